@@ -1,0 +1,102 @@
+/*
+ * metellus_hip.h -- C ABI of the MI355X (gfx950) native shim.
+ *
+ * Replaces the reference's Objective-C++/nanobind module `metal_backend`
+ * (reference: src/metal_backend.mm:253-261), whose seven Python functions are
+ * create_buffer, release_buffer, buffer_size, write_buffer, read_buffer,
+ * fill_buffer and run_kernel.  Here run_kernel is split into a cached compile
+ * (mt_compile) and a launch (mt_launch); the Python wrapper
+ * metellus_amd/runtime/hip_backend.py rebuilds the seven functions on top.
+ *
+ * Conventions
+ *   - Every function returns 0 on success and nonzero on failure; the message
+ *     of the calling thread's last failure is returned by mt_last_error().
+ *   - Buffers are opaque handles >= 1 owned by the shim's registry.
+ *   - All device work is ordered on one HIP stream (default priority).
+ *     mt_read, mt_sync and timed launches synchronise; everything else is
+ *     asynchronous and stream-ordered (frees included).
+ *   - Plain pointers and sizes only; no framework types cross this boundary.
+ */
+#ifndef METELLUS_HIP_H
+#define METELLUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of this thread's last failure ("" if none). */
+const char* mt_last_error(void);
+
+/* Select device 0 and create the stream.  Idempotent; called implicitly. */
+int mt_init(void);
+
+/* Number of visible HIP devices (0 on a machine without a GPU). */
+int mt_device_count(int* count);
+
+/* Target id of device 0 (e.g. "gfx950:sramecc+:xnack-"), compute-unit count
+ * and peak clock in kHz. */
+int mt_device_info(char* arch, size_t arch_len, int* cu_count, int* clock_khz);
+
+/* create_buffer (reference: src/metal_backend.mm:94-99): nbytes must be > 0. */
+int mt_alloc(size_t nbytes, uint64_t* handle);
+
+/* release_buffer (reference: src/metal_backend.mm:101-103): *existed is 1 if
+ * the handle was live, 0 if unknown/already released (not an error). */
+int mt_free(uint64_t handle, int* existed);
+
+/* buffer_size (reference: src/metal_backend.mm:105-108). */
+int mt_size(uint64_t handle, size_t* nbytes);
+
+/* Device address of a buffer (for callers that launch their own work). */
+int mt_device_ptr(uint64_t handle, uint64_t* address);
+
+/* write_buffer (reference: src/metal_backend.mm:110-117): copies nbytes from
+ * host memory; nbytes must not exceed the buffer size.  Returns after the
+ * copy completed. */
+int mt_write(uint64_t handle, const void* src, size_t nbytes);
+
+/* read_buffer (reference: src/metal_backend.mm:119-126): waits for all
+ * queued work, then copies nbytes to host memory. */
+int mt_read(uint64_t handle, void* dst, size_t nbytes);
+
+/* fill_buffer (reference: src/metal_backend.mm:128-141): byte fill. */
+int mt_fill(uint64_t handle, uint8_t value);
+
+/* First half of run_kernel (reference: src/metal_backend.mm:178-207):
+ * compile `source` with hiprtc for the device's target, load it and look up
+ * `function_name`.  Code objects are cached in memory (and on disk unless
+ * MT_KERNEL_CACHE=0) by the exact (source, function, options, target) key,
+ * so repeated dispatches do not recompile.  `options` is a space-separated
+ * list appended to the defaults (-O3 -std=c++17 -ffp-contract=off, packed
+ * fp32 ops disabled). */
+int mt_compile(const char* source, const char* function_name, const char* options, uint64_t* kernel);
+
+/* Compile only (no device needed): returns the code-object size for the
+ * given target ("gfx950" when NULL).  Used to check generated kernels build
+ * on a machine without a GPU. */
+int mt_compile_only(const char* source, const char* options, const char* target, size_t* code_size);
+
+/* Second half of run_kernel (reference: src/metal_backend.mm:209-249):
+ * launch grid[0..2] workgroups of block[0..2] lanes.  The kernel's
+ * parameters are the nbuf buffers in order with the `ndims` uint32 dims
+ * (passed by value as a 16-word struct) inserted at position dims_slot.
+ * When timed != 0 the launch is bracketed by HIP events on the shim's stream
+ * and *ms receives the kernel time after synchronising. */
+int mt_launch(uint64_t kernel, const uint64_t* buffers, int nbuf, const uint32_t* dims, int ndims,
+              int dims_slot, const uint32_t* grid, const uint32_t* block, int timed, float* ms);
+
+/* Wait for all queued work on the shim's stream. */
+int mt_sync(void);
+
+/* Number of kernels compiled by hiprtc in this process (cache misses) and
+ * served from a cache (hits); for tests of the cache. */
+int mt_cache_stats(uint64_t* compiled, uint64_t* hits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* METELLUS_HIP_H */

@@ -1,0 +1,127 @@
+"""gfx950 matmul tile policy.
+
+Replaces the reference's Apple tile picker (reference:
+src/compute/matmul/config.py:40-51: 32x32x16 .. 128x64x32 tiles, four
+32-wide simdgroups).  Here a workgroup of ``sg_M x sg_N`` wave64s computes a
+``tile_M x tile_N`` output tile with fp32 MFMA (32x32 blocks); each wave owns
+a ``(tile_M/sg_M) x (tile_N/sg_N)`` sub-tile, i.e. ``WM x WN`` accumulator
+blocks of 16 registers.  A and B k-chunks of ``tile_K`` are double-buffered
+in LDS (rows padded by ``a_pad``/``b_pad`` floats to spread LDS banks).
+
+``select_tile_config`` takes the largest tile that still yields at least one
+workgroup per compute unit (256 on MI355X); shapes too small for that get the
+tile giving the most workgroups.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+NUM_CUS = 256  # MI355X compute units (8 XCDs x 32)
+
+
+@dataclass(frozen=True)
+class TileConfig:
+    tile_M: int
+    tile_N: int
+    tile_K: int
+    sg_M: int  # waves along M
+    sg_N: int  # waves along N
+    a_pad: int = 4
+    b_pad: int = 4
+    stages: int = 2
+
+    @property
+    def num_threads(self) -> int:
+        return 64 * self.sg_M * self.sg_N
+
+    @property
+    def tg_x(self) -> int:
+        return self.num_threads
+
+    @property
+    def tg_y(self) -> int:
+        return 1
+
+    @property
+    def wave_M(self) -> int:
+        return self.tile_M // self.sg_M
+
+    @property
+    def wave_N(self) -> int:
+        return self.tile_N // self.sg_N
+
+    @property
+    def WM(self) -> int:
+        return self.wave_M // 32
+
+    @property
+    def WN(self) -> int:
+        return self.wave_N // 32
+
+    @property
+    def lda(self) -> int:
+        return self.tile_K + self.a_pad
+
+    @property
+    def ldb(self) -> int:
+        return self.tile_N + self.b_pad
+
+    def a_tile_shape(self) -> tuple[int, ...]:
+        return (self.stages, self.tile_M, self.lda)
+
+    def b_tile_shape(self) -> tuple[int, ...]:
+        return (self.stages, self.tile_K, self.ldb)
+
+    def validate(self) -> None:
+        if self.wave_M % 32 or self.wave_N % 32 or self.tile_M % self.sg_M or self.tile_N % self.sg_N:
+            raise ValueError(f"wave tile must be a multiple of 32x32: {self}")
+        if self.tile_K % 8:
+            raise ValueError(f"tile_K must be a multiple of 8: {self}")
+        if self.lda % 4 or self.ldb % 4:
+            raise ValueError(f"LDS row pitch must be a multiple of 4 floats: {self}")
+        if self.num_threads > 1024:
+            raise ValueError(f"at most 1024 lanes per workgroup: {self}")
+
+
+def ceil_div(a: int, b: int) -> int:
+    return (a + b - 1) // b
+
+
+def is_aligned_shape(M: int, K: int, N: int, config: TileConfig) -> bool:
+    return M % config.tile_M == 0 and N % config.tile_N == 0 and K % config.tile_K == 0
+
+
+def grid_for(M: int, N: int, config: TileConfig) -> tuple[int, int, int]:
+    return (ceil_div(N, config.tile_N), ceil_div(M, config.tile_M), 1)
+
+
+# Largest first.  One accumulator set: wave tiles up to 128x64 (128 acc regs).
+SINGLE_ANCHOR_TILES = (
+    TileConfig(256, 256, 32, 2, 4),
+    TileConfig(256, 128, 32, 2, 2),
+    TileConfig(128, 256, 32, 2, 2),
+    TileConfig(128, 128, 32, 2, 2),
+    TileConfig(128, 64, 32, 2, 2),
+    TileConfig(64, 128, 32, 2, 2),
+    TileConfig(64, 64, 32, 2, 2),
+    TileConfig(32, 32, 32, 1, 1),
+)
+
+# Two accumulator sets (multi-anchor): wave tiles up to 64x64 per anchor.
+DUAL_ANCHOR_TILES = (
+    TileConfig(256, 128, 32, 4, 2),
+    TileConfig(128, 128, 32, 2, 2),
+    TileConfig(128, 64, 32, 2, 2),
+    TileConfig(64, 128, 32, 2, 2),
+    TileConfig(64, 64, 32, 2, 2),
+    TileConfig(32, 32, 32, 1, 1),
+)
+
+
+def select_tile_config(M: int, K: int, N: int, anchors: int = 1) -> TileConfig:
+    cands = SINGLE_ANCHOR_TILES if anchors == 1 else DUAL_ANCHOR_TILES
+    for t in cands:
+        if ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N) >= NUM_CUS:
+            return t
+    return max(cands, key=lambda t: (ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N), -t.tile_M * t.tile_N))

@@ -1,0 +1,265 @@
+// mt_device.h -- hand-written gfx950 (CDNA4) device library.
+//
+// Prepended to every kernel the fragment compiler generates, then compiled
+// by hiprtc.  Generated code composes these pieces; the fused elementwise
+// expressions arrive as lambdas (prologue transforms, epilogues, merges).
+//
+//   * mt_dims                 dims passed by value in the kernel arguments
+//   * mt_ld4 / mt_st4         128-bit global loads / stores
+//   * mt_wave_*               wave64 butterfly reductions (fixed order)
+//   * mt_tile_colvec / rowvec / scalar
+//                             cooperative ROWS x COLS tile fetch: global ->
+//                             registers (transform applied to in-bounds
+//                             elements, 0 outside), then registers -> LDS
+//   * mt_mfma_tile            fp32 MFMA (v_mfma_f32_32x32x2f32) over one LDS
+//                             k-chunk for a wave's WM x WN grid of 32x32 blocks
+//   * mt_acc_row              row of accumulator register v in a 32x32 block
+//
+// All indices are unsigned 32-bit except global offsets (size_t).
+
+typedef float mt_f32x4 __attribute__((ext_vector_type(4)));
+typedef float mt_f32x16 __attribute__((ext_vector_type(16)));
+
+struct mt_dims {
+    unsigned int v[16];
+};
+
+#define MT_INLINE __device__ __forceinline__
+
+#ifndef INFINITY
+#define INFINITY __builtin_inff()
+#endif
+#ifndef NAN
+#define NAN __builtin_nanf("")
+#endif
+
+MT_INLINE mt_f32x4 mt_ld4(const float* p) { return *reinterpret_cast<const mt_f32x4*>(p); }
+MT_INLINE void mt_st4(float* p, mt_f32x4 v) { *reinterpret_cast<mt_f32x4*>(p) = v; }
+
+MT_INLINE unsigned mt_lane() { return threadIdx.x & 63u; }
+// Wave index as a scalar (wave-uniform) value.
+MT_INLINE unsigned mt_wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// ---------------------------------------------------------------------------
+// wave64 reductions.  Butterfly over xor offsets 32, 16, 8, 4, 2, 1: after
+// step `off`, lane l holds v_l (op) v_{l^off}.  Every lane ends with the same
+// value; the pairing tree is fixed, so results are reproducible (and the CPU
+// oracle replays the same tree).
+// ---------------------------------------------------------------------------
+
+MT_INLINE float mt_shfl_xor(float v, int off) { return __shfl_xor(v, off, 64); }
+
+MT_INLINE float mt_wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = v + mt_shfl_xor(v, off);
+    return v;
+}
+MT_INLINE float mt_wave_product(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = v * mt_shfl_xor(v, off);
+    return v;
+}
+MT_INLINE float mt_wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, mt_shfl_xor(v, off));
+    return v;
+}
+MT_INLINE float mt_wave_min(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fminf(v, mt_shfl_xor(v, off));
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Cooperative tile loaders.  A loader owns the registers for its share of one
+// ROWS x COLS tile (NT lanes).  fetch<CHECK>() issues the global loads for the
+// tile at (row0, col0) of a strided matrix (element (r, c) at
+// src[r*rs + c*cs]); F(raw, row, col) transforms each in-bounds element
+// (elementwise prologue); elements outside (rlim, clim) are 0 (identity of
+// the matmul / sum consumer).  commit<LD>() writes the registers into an LDS
+// tile with row pitch LD floats.  Splitting the two lets the mainloop keep
+// the next tile's loads in flight while the MFMAs run.
+// ---------------------------------------------------------------------------
+
+struct mt_identity {
+    MT_INLINE float operator()(float v, unsigned, unsigned) const { return v; }
+};
+
+// Vectorised along columns: cs == 1, rs % 4 == 0, COLS % 4 == 0, clim % 4 == 0.
+template <int ROWS, int COLS, int NT>
+struct mt_tile_colvec {
+    static constexpr int CV = COLS / 4;
+    static constexpr int TOTAL = ROWS * CV;
+    static constexpr int PER = (TOTAL + NT - 1) / NT;
+    mt_f32x4 v[PER];
+
+    template <bool CHECK, typename F>
+    MT_INLINE void fetch(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
+                         unsigned rlim, unsigned clim, unsigned tid, F f) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / CV, c = (idx % CV) * 4u;
+            const unsigned gr = row0 + r, gc = col0 + c;
+            mt_f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rlim && gc < clim))) {
+                x = mt_ld4(src + (size_t)gr * rs + gc);
+                x.x = f(x.x, gr, gc);
+                x.y = f(x.y, gr, gc + 1u);
+                x.z = f(x.z, gr, gc + 2u);
+                x.w = f(x.w, gr, gc + 3u);
+            }
+            v[i] = x;
+        }
+    }
+
+    template <int LD>
+    MT_INLINE void commit(float* lds, unsigned tid) const {
+        static_assert(LD % 4 == 0, "colvec commit needs a 16-byte row pitch");
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            if (TOTAL % NT == 0 || idx < (unsigned)TOTAL) {
+                const unsigned r = idx / CV, c = (idx % CV) * 4u;
+                mt_st4(lds + r * LD + c, v[i]);
+            }
+        }
+    }
+};
+
+// Vectorised along rows: rs == 1, cs % 4 == 0, ROWS % 4 == 0, rlim % 4 == 0.
+template <int ROWS, int COLS, int NT>
+struct mt_tile_rowvec {
+    static constexpr int RV = ROWS / 4;
+    static constexpr int TOTAL = RV * COLS;
+    static constexpr int PER = (TOTAL + NT - 1) / NT;
+    mt_f32x4 v[PER];
+
+    template <bool CHECK, typename F>
+    MT_INLINE void fetch(const float* __restrict__ src, unsigned cs, unsigned row0, unsigned col0,
+                         unsigned rlim, unsigned clim, unsigned tid, F f) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned c = idx / RV, r = (idx % RV) * 4u;
+            const unsigned gr = row0 + r, gc = col0 + c;
+            mt_f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rlim && gc < clim))) {
+                x = mt_ld4(src + gr + (size_t)gc * cs);
+                x.x = f(x.x, gr, gc);
+                x.y = f(x.y, gr + 1u, gc);
+                x.z = f(x.z, gr + 2u, gc);
+                x.w = f(x.w, gr + 3u, gc);
+            }
+            v[i] = x;
+        }
+    }
+
+    template <int LD>
+    MT_INLINE void commit(float* lds, unsigned tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            if (TOTAL % NT == 0 || idx < (unsigned)TOTAL) {
+                const unsigned c = idx / RV, r = (idx % RV) * 4u;
+                lds[(r + 0u) * LD + c] = v[i].x;
+                lds[(r + 1u) * LD + c] = v[i].y;
+                lds[(r + 2u) * LD + c] = v[i].z;
+                lds[(r + 3u) * LD + c] = v[i].w;
+            }
+        }
+    }
+};
+
+// Any strides: one element per load.
+template <int ROWS, int COLS, int NT>
+struct mt_tile_scalar {
+    static constexpr int TOTAL = ROWS * COLS;
+    static constexpr int PER = (TOTAL + NT - 1) / NT;
+    float v[PER];
+
+    template <bool CHECK, typename F>
+    MT_INLINE void fetch(const float* __restrict__ src, unsigned rs, unsigned cs, unsigned row0,
+                         unsigned col0, unsigned rlim, unsigned clim, unsigned tid, F f) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / COLS, c = idx % COLS;
+            const unsigned gr = row0 + r, gc = col0 + c;
+            float x = 0.f;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rlim && gc < clim))) {
+                x = f(src[(size_t)gr * rs + (size_t)gc * cs], gr, gc);
+            }
+            v[i] = x;
+        }
+    }
+
+    template <int LD>
+    MT_INLINE void commit(float* lds, unsigned tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            if (TOTAL % NT == 0 || idx < (unsigned)TOTAL) {
+                const unsigned r = idx / COLS, c = idx % COLS;
+                lds[r * LD + c] = v[i];
+            }
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// fp32 MFMA over one LDS k-chunk.
+//
+// v_mfma_f32_32x32x2f32 computes D[32x32] += A[32x2] * B[2x32]; lane l supplies
+// A[l%32][l/32] and B[l/32][l%32].  The two k slots of one instruction are
+// taken from the two halves of the chunk: lane half h = l/32 feeds chunk
+// column k = h*TK/2 + s at step s.  Both operands use the same mapping, so
+// every product A[i][k]*B[k][j] of the chunk is accumulated exactly once, and
+// consecutive steps s read consecutive A elements (128-bit LDS reads).
+//
+// As points at the wave's first A row in an LDS tile [rows][LDA] (row-major,
+// m x k); Bs at the wave's first column in an LDS tile [TK][LDB] (k x n).
+// acc[i][j] is the 32x32 block at rows 32*i, cols 32*j of the wave tile.
+// ---------------------------------------------------------------------------
+
+template <int WM, int WN, int TK, int LDA, int LDB>
+MT_INLINE void mt_mfma_tile(const float* __restrict__ As, const float* __restrict__ Bs,
+                            mt_f32x16 (&acc)[WM][WN], unsigned lane) {
+    static_assert(TK % 8 == 0, "TK must be a multiple of 8");
+    static_assert(LDA % 4 == 0, "LDA must keep 16-byte alignment");
+    constexpr int HALF = TK / 2;
+    const unsigned li = lane & 31u;
+    const unsigned lh = lane >> 5;
+    const float* a_base = As + li * LDA + lh * HALF;
+    const float* b_base = Bs + (lh * HALF) * LDB + li;
+#pragma unroll
+    for (int s0 = 0; s0 < HALF; s0 += 4) {
+        mt_f32x4 a[WM];
+#pragma unroll
+        for (int i = 0; i < WM; ++i) a[i] = mt_ld4(a_base + i * 32 * LDA + s0);
+#pragma unroll
+        for (int ss = 0; ss < 4; ++ss) {
+            float b[WN];
+#pragma unroll
+            for (int j = 0; j < WN; ++j) b[j] = b_base[(s0 + ss) * LDB + j * 32];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+#pragma unroll
+                for (int j = 0; j < WN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][ss], b[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    }
+}
+
+// Row (within a 32x32 output block) of accumulator register v held by `lane`;
+// the column is lane % 32.
+MT_INLINE unsigned mt_acc_row(int v, unsigned lane) {
+    return 8u * (unsigned)(v >> 2) + 4u * (lane >> 5) + (unsigned)(v & 3);
+}
+
+MT_INLINE void mt_zero(mt_f32x16& a) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a[i] = 0.f;
+}

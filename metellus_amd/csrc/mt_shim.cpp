@@ -1,0 +1,447 @@
+// mt_shim.cpp -- native C-ABI shim for the MI355X backend (declarations and
+// contract: include/metellus_hip.h).
+//
+// Replaces the reference's Metal backend (reference: src/metal_backend.mm):
+//   * a buffer registry of stream-ordered device allocations (hipMallocAsync /
+//     hipFreeAsync), opaque u64 handles starting at 1;
+//   * hiprtc compilation of generated kernels with an in-memory and on-disk
+//     code-object cache keyed by the exact (source, function, options, target)
+//     text -- the reference recompiled MSL on every dispatch
+//     (metal_backend.mm:188-207);
+//   * hipModuleLaunchKernel on a single stream, asynchronous unless timed --
+//     the reference waited after every dispatch (metal_backend.mm:226-227).
+//
+// Pure host code: it contains no device kernels of its own.
+
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <sys/stat.h>
+#include <unistd.h>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/metellus_hip.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(const std::string& msg) {
+    g_error = msg;
+    return 1;
+}
+
+#define MT_HIP(call)                                                                      \
+    do {                                                                                  \
+        hipError_t e_ = (call);                                                           \
+        if (e_ != hipSuccess) {                                                           \
+            return fail(std::string(#call) + " failed: " + hipGetErrorString(e_));        \
+        }                                                                                 \
+    } while (0)
+
+constexpr int kMaxDims = 16;
+struct DimsArg {
+    uint32_t v[kMaxDims];
+};
+
+struct Buffer {
+    void* ptr;
+    size_t nbytes;
+};
+
+struct Kernel {
+    hipModule_t module;
+    hipFunction_t function;
+};
+
+struct State {
+    std::mutex mu;
+    bool ready = false;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev_start = nullptr;
+    hipEvent_t ev_stop = nullptr;
+    std::string arch;  // full target id of device 0
+    int cu_count = 0;
+    int clock_khz = 0;
+    std::unordered_map<uint64_t, Buffer> buffers;
+    uint64_t next_buffer = 1;
+    std::vector<Kernel> kernels;                       // handle = index + 1
+    std::unordered_map<std::string, uint64_t> by_key;  // exact key -> handle
+    uint64_t compiled = 0;
+    uint64_t hits = 0;
+};
+
+State& state() {
+    static State s;
+    return s;
+}
+
+// Caller holds s.mu.
+int init_locked(State& s) {
+    if (s.ready) return 0;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+        return fail(std::string("no HIP device available: ") +
+                    (e != hipSuccess ? hipGetErrorString(e) : "device count is 0"));
+    }
+    MT_HIP(hipSetDevice(0));
+    hipDeviceProp_t prop;
+    MT_HIP(hipGetDeviceProperties(&prop, 0));
+    s.arch = prop.gcnArchName;
+    s.cu_count = prop.multiProcessorCount;
+    s.clock_khz = prop.clockRate;
+    MT_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
+    MT_HIP(hipEventCreate(&s.ev_start));
+    MT_HIP(hipEventCreate(&s.ev_stop));
+    s.ready = true;
+    return 0;
+}
+
+// ---- hiprtc -----------------------------------------------------------------
+
+std::vector<std::string> split_options(const char* opts) {
+    std::vector<std::string> out;
+    if (opts == nullptr) return out;
+    std::string cur;
+    for (const char* p = opts; *p; ++p) {
+        if (*p == ' ' || *p == '\t' || *p == '\n') {
+            if (!cur.empty()) out.push_back(cur), cur.clear();
+        } else {
+            cur.push_back(*p);
+        }
+    }
+    if (!cur.empty()) out.push_back(cur);
+    return out;
+}
+
+std::vector<std::string> full_options(const std::string& target, const char* extra) {
+    std::vector<std::string> o = {
+        "--offload-arch=" + target,
+        "-O3",
+        "-std=c++17",
+        "-ffp-contract=off",
+        // Packed fp32 VALU forms are disabled for every kernel on this pool.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    };
+    for (auto& x : split_options(extra)) o.push_back(x);
+    return o;
+}
+
+int rtc_compile(const std::string& source, const std::vector<std::string>& options,
+                std::vector<char>* code) {
+    hiprtcProgram prog;
+    hiprtcResult r = hiprtcCreateProgram(&prog, source.c_str(), "metellus_kernel.hip", 0, nullptr, nullptr);
+    if (r != HIPRTC_SUCCESS) return fail(std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r));
+    std::vector<const char*> argv;
+    for (auto& s : options) argv.push_back(s.c_str());
+    r = hiprtcCompileProgram(prog, static_cast<int>(argv.size()), argv.data());
+    if (r != HIPRTC_SUCCESS) {
+        size_t n = 0;
+        hiprtcGetProgramLogSize(prog, &n);
+        std::string log(n, '\0');
+        if (n) hiprtcGetProgramLog(prog, &log[0]);
+        hiprtcDestroyProgram(&prog);
+        return fail(std::string("hiprtc compile failed: ") + hiprtcGetErrorString(r) + "\n" + log);
+    }
+    size_t n = 0;
+    hiprtcGetCodeSize(prog, &n);
+    code->resize(n);
+    hiprtcGetCode(prog, code->data());
+    hiprtcDestroyProgram(&prog);
+    return 0;
+}
+
+uint64_t fnv1a(const std::string& s) {
+    uint64_t h = 1469598103934665603ull;
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+std::string cache_dir() {
+    const char* flag = std::getenv("MT_KERNEL_CACHE");
+    if (flag && std::string(flag) == "0") return "";
+    const char* dir = std::getenv("MT_KERNEL_CACHE_DIR");
+    if (dir && *dir) return dir;
+    const char* home = std::getenv("HOME");
+    if (!home || !*home) return "";
+    return std::string(home) + "/.cache/metellus_amd";
+}
+
+void mkdirs(const std::string& path) {
+    std::string cur;
+    for (size_t i = 0; i < path.size(); ++i) {
+        cur.push_back(path[i]);
+        if (path[i] == '/' || i + 1 == path.size()) mkdir(cur.c_str(), 0755);
+    }
+}
+
+bool disk_load(const std::string& file, std::vector<char>* code) {
+    FILE* f = std::fopen(file.c_str(), "rb");
+    if (!f) return false;
+    std::fseek(f, 0, SEEK_END);
+    long n = std::ftell(f);
+    std::fseek(f, 0, SEEK_SET);
+    bool ok = n > 0;
+    if (ok) {
+        code->resize(static_cast<size_t>(n));
+        ok = std::fread(code->data(), 1, code->size(), f) == code->size();
+    }
+    std::fclose(f);
+    return ok;
+}
+
+void disk_store(const std::string& dir, const std::string& file, const std::vector<char>& code) {
+    mkdirs(dir);
+    std::string tmp = file + ".tmp" + std::to_string(static_cast<long>(getpid()));
+    FILE* f = std::fopen(tmp.c_str(), "wb");
+    if (!f) return;
+    bool ok = std::fwrite(code.data(), 1, code.size(), f) == code.size();
+    std::fclose(f);
+    if (ok) std::rename(tmp.c_str(), file.c_str());
+    else std::remove(tmp.c_str());
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mt_last_error(void) { return g_error.c_str(); }
+
+int mt_init(void) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    return init_locked(s);
+}
+
+int mt_device_count(int* count) {
+    if (!count) return fail("mt_device_count: null output");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *count = (e == hipSuccess) ? n : 0;
+    return 0;
+}
+
+int mt_device_info(char* arch, size_t arch_len, int* cu_count, int* clock_khz) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    if (arch && arch_len) {
+        std::strncpy(arch, s.arch.c_str(), arch_len - 1);
+        arch[arch_len - 1] = '\0';
+    }
+    if (cu_count) *cu_count = s.cu_count;
+    if (clock_khz) *clock_khz = s.clock_khz;
+    return 0;
+}
+
+int mt_alloc(size_t nbytes, uint64_t* handle) {
+    if (!handle) return fail("mt_alloc: null output");
+    if (nbytes == 0) return fail("create_buffer: nbytes must be > 0");
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    void* p = nullptr;
+    MT_HIP(hipMallocAsync(&p, nbytes, s.stream));
+    uint64_t h = s.next_buffer++;
+    s.buffers.emplace(h, Buffer{p, nbytes});
+    *handle = h;
+    return 0;
+}
+
+int mt_free(uint64_t handle, int* existed) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    auto it = s.buffers.find(handle);
+    if (it == s.buffers.end()) {
+        if (existed) *existed = 0;
+        return 0;
+    }
+    void* p = it->second.ptr;
+    s.buffers.erase(it);
+    if (existed) *existed = 1;
+    // Stream-ordered: kernels already queued that read the buffer finish first.
+    MT_HIP(hipFreeAsync(p, s.stream));
+    return 0;
+}
+
+static int lookup(State& s, uint64_t handle, Buffer* out) {
+    auto it = s.buffers.find(handle);
+    if (it == s.buffers.end()) return fail("Unknown buffer handle: " + std::to_string(handle));
+    *out = it->second;
+    return 0;
+}
+
+int mt_size(uint64_t handle, size_t* nbytes) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    Buffer b;
+    if (lookup(s, handle, &b)) return 1;
+    if (nbytes) *nbytes = b.nbytes;
+    return 0;
+}
+
+int mt_device_ptr(uint64_t handle, uint64_t* address) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    Buffer b;
+    if (lookup(s, handle, &b)) return 1;
+    if (address) *address = reinterpret_cast<uint64_t>(b.ptr);
+    return 0;
+}
+
+int mt_write(uint64_t handle, const void* src, size_t nbytes) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    Buffer b;
+    if (lookup(s, handle, &b)) return 1;
+    if (nbytes > b.nbytes) return fail("write_buffer: source larger than buffer");
+    if (nbytes == 0) return 0;
+    MT_HIP(hipMemcpyAsync(b.ptr, src, nbytes, hipMemcpyHostToDevice, s.stream));
+    MT_HIP(hipStreamSynchronize(s.stream));
+    return 0;
+}
+
+int mt_read(uint64_t handle, void* dst, size_t nbytes) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    Buffer b;
+    if (lookup(s, handle, &b)) return 1;
+    if (nbytes > b.nbytes) return fail("read_buffer: destination larger than buffer");
+    if (nbytes == 0) return 0;
+    MT_HIP(hipMemcpyAsync(dst, b.ptr, nbytes, hipMemcpyDeviceToHost, s.stream));
+    MT_HIP(hipStreamSynchronize(s.stream));
+    return 0;
+}
+
+int mt_fill(uint64_t handle, uint8_t value) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    Buffer b;
+    if (lookup(s, handle, &b)) return 1;
+    MT_HIP(hipMemsetAsync(b.ptr, value, b.nbytes, s.stream));
+    return 0;
+}
+
+int mt_compile_only(const char* source, const char* options, const char* target, size_t* code_size) {
+    if (!source) return fail("mt_compile_only: null source");
+    std::vector<char> code;
+    std::string t = (target && *target) ? target : "gfx950";
+    if (rtc_compile(source, full_options(t, options), &code)) return 1;
+    if (code_size) *code_size = code.size();
+    return 0;
+}
+
+int mt_compile(const char* source, const char* function_name, const char* options, uint64_t* kernel) {
+    if (!source || !function_name || !kernel) return fail("mt_compile: null argument");
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    std::vector<std::string> opts = full_options(s.arch, options);
+    std::string key;
+    key.reserve(std::strlen(source) + 256);
+    key.append(source).push_back('\0');
+    key.append(function_name).push_back('\0');
+    for (auto& o : opts) key.append(o).push_back(' ');
+    auto hit = s.by_key.find(key);
+    if (hit != s.by_key.end()) {
+        ++s.hits;
+        *kernel = hit->second;
+        return 0;
+    }
+    std::vector<char> code;
+    std::string dir = cache_dir();
+    char name[32];
+    std::snprintf(name, sizeof(name), "%016llx.co", static_cast<unsigned long long>(fnv1a(key)));
+    std::string file = dir.empty() ? "" : dir + "/" + name;
+    if (!file.empty() && disk_load(file, &code)) {
+        ++s.hits;
+    } else {
+        if (rtc_compile(source, opts, &code)) return 1;
+        ++s.compiled;
+        if (!file.empty()) disk_store(dir, file, code);
+    }
+    Kernel k{};
+    MT_HIP(hipModuleLoadData(&k.module, code.data()));
+    hipError_t e = hipModuleGetFunction(&k.function, k.module, function_name);
+    if (e != hipSuccess) {
+        (void)hipModuleUnload(k.module);
+        return fail(std::string("kernel function was not found: ") + function_name + " (" +
+                    hipGetErrorString(e) + ")");
+    }
+    s.kernels.push_back(k);
+    uint64_t h = s.kernels.size();
+    s.by_key.emplace(std::move(key), h);
+    *kernel = h;
+    return 0;
+}
+
+int mt_launch(uint64_t kernel, const uint64_t* buffers, int nbuf, const uint32_t* dims, int ndims,
+              int dims_slot, const uint32_t* grid, const uint32_t* block, int timed, float* ms) {
+    if (!grid || !block) return fail("mt_launch: grid and block are required");
+    if (ndims < 0 || ndims > kMaxDims) return fail("mt_launch: at most 16 dims");
+    if (nbuf < 0 || dims_slot < 0 || dims_slot > nbuf) return fail("mt_launch: bad dims slot");
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    if (kernel == 0 || kernel > s.kernels.size()) return fail("mt_launch: unknown kernel handle");
+    for (int i = 0; i < 3; ++i) {
+        if (grid[i] == 0 || block[i] == 0) return fail("mt_launch: zero grid or block extent");
+    }
+    if (static_cast<uint64_t>(block[0]) * block[1] * block[2] > 1024)
+        return fail("mt_launch: more than 1024 lanes per workgroup");
+    std::vector<void*> ptrs(static_cast<size_t>(nbuf));
+    for (int i = 0; i < nbuf; ++i) {
+        Buffer b;
+        if (lookup(s, buffers[i], &b)) return 1;
+        ptrs[i] = b.ptr;
+    }
+    DimsArg d{};
+    for (int i = 0; i < ndims; ++i) d.v[i] = dims[i];
+    std::vector<void*> params;
+    params.reserve(static_cast<size_t>(nbuf) + 1);
+    for (int i = 0; i <= nbuf; ++i) {
+        if (i == dims_slot) params.push_back(&d);
+        if (i < nbuf) params.push_back(&ptrs[i]);
+    }
+    const Kernel& k = s.kernels[kernel - 1];
+    if (timed) MT_HIP(hipEventRecord(s.ev_start, s.stream));
+    MT_HIP(hipModuleLaunchKernel(k.function, grid[0], grid[1], grid[2], block[0], block[1], block[2], 0,
+                                 s.stream, params.data(), nullptr));
+    if (timed) {
+        MT_HIP(hipEventRecord(s.ev_stop, s.stream));
+        MT_HIP(hipEventSynchronize(s.ev_stop));
+        float t = 0.f;
+        MT_HIP(hipEventElapsedTime(&t, s.ev_start, s.ev_stop));
+        if (ms) *ms = t;
+    }
+    return 0;
+}
+
+int mt_sync(void) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    MT_HIP(hipStreamSynchronize(s.stream));
+    return 0;
+}
+
+int mt_cache_stats(uint64_t* compiled, uint64_t* hits) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (compiled) *compiled = s.compiled;
+    if (hits) *hits = s.hits;
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,170 @@
+"""Matmul strategy: standalone, prologue-fused, tile- or register-epilogue
+matmul (reference: src/orchestrator/assembly/matmul.py:33-285).
+
+Kept from the reference: the strategy labels, the bindings (deduplicated
+device inputs A/B, then the final output, then extra operands in order of
+first use), dims ``(M, K, N)``, grid ``(N tiles, M tiles, 1)``, operand
+strides read from the ``Tensor`` metadata (transposed views load
+transposed; K^T is read along K with 128-bit loads, no transpose kernel).
+
+gfx950 kernel: fp32 MFMA mainloop over double-buffered LDS, every epilogue
+applied to the accumulator registers (both ``MATMUL_EPILOGUE_REGISTER`` and
+``MATMUL_EPILOGUE_TG``; the label records the reference's decision), then a
+direct store.  LDS holds only the A and B chunks.
+"""
+
+from __future__ import annotations
+
+from metellus_amd.compute.fragments import BarrierFragment, CodegenContext, lds_decl
+from metellus_amd.compute.matmul.config import TileConfig, grid_for, is_aligned_shape, select_tile_config
+from metellus_amd.compute.matmul.matmul import (
+    MatmulComputeFragment,
+    MatmulConfig,
+    MatmulEpilogueStoreFragment,
+    MatmulMainloopFragment,
+    MatmulSetupFragment,
+    MatmulTileMappingFragment,
+    ThreadIndexFragment,
+)
+from metellus_amd.memory.memory import TgLoadFragment
+from metellus_amd.orchestrator.assembly.decision import DecisionView
+from metellus_amd.orchestrator.assembly.expressions import ChainCode
+from metellus_amd.orchestrator.assembly.extras import Extras, input_param, output_param, param_name
+from metellus_amd.orchestrator.ir import MatmulOp, Tensor
+from metellus_amd.orchestrator.kernel_group import KernelGroup
+from metellus_amd.runtime.program import Kernel
+
+
+def operand_load(
+    *,
+    name: str,
+    src: Tensor,
+    dst: str,
+    tile: TileConfig,
+    side: str,
+    M: int,
+    K: int,
+    N: int,
+    aligned: bool,
+    k_limit: str = "K",
+    prologue: ChainCode | None = None,
+) -> TgLoadFragment:
+    """Loader for the A (side "a": tile_M x tile_K at (tile_m0, k_chunk)) or
+    B (side "b": tile_K x tile_N at (k_chunk, tile_n0)) operand."""
+    rs, cs = src.row_stride, src.col_stride
+    if side == "a":
+        shape, pitch = (tile.tile_M, tile.tile_K), tile.lda
+        row_start, col_start = "tile_m0", "k_chunk"
+        row_lim, col_lim = "M", k_limit
+        rows_total, cols_total = M, K
+    else:
+        shape, pitch = (tile.tile_K, tile.tile_N), tile.ldb
+        row_start, col_start = "k_chunk", "tile_n0"
+        row_lim, col_lim = k_limit, "N"
+        rows_total, cols_total = K, N
+    if cs == 1 and rs % 4 == 0 and cols_total % 4 == 0:
+        mode = "colvec"
+    elif rs == 1 and cs % 4 == 0 and rows_total % 4 == 0:
+        mode = "rowvec"
+    else:
+        mode = "scalar"
+    lam = prologue.lambda_transform() if prologue is not None else None
+    return TgLoadFragment(
+        name=name,
+        src_name=param_name(src.buffer_key),
+        src_row_stride=str(rs),
+        src_col_stride=str(cs),
+        row_start=row_start,
+        col_start=col_start,
+        dst_name=dst,
+        tile_shape=shape,
+        num_threads=tile.num_threads,
+        row_limit=None if aligned else row_lim,
+        col_limit=None if aligned else col_lim,
+        dst_pitch=pitch,
+        stages=tile.stages,
+        mode=mode,
+        transform_lambda=lam,
+    )
+
+
+def assemble_matmul(decision: DecisionView, function_name: str | None) -> KernelGroup:
+    anchor = decision.anchor
+    assert isinstance(anchor, MatmulOp)
+    src_a = decision.prologue_a[0].operands[0] if decision.prologue_a else anchor.a
+    src_b = decision.prologue_b[0].operands[0] if decision.prologue_b else anchor.b
+    assert isinstance(src_a, Tensor) and isinstance(src_b, Tensor)
+    M, K = anchor.a.shape
+    N = anchor.b.shape[1]
+    tile = select_tile_config(M, K, N)
+    aligned = is_aligned_shape(M, K, N, tile)
+    final_out = decision.epilogue[-1].out if decision.epilogue else anchor.out
+    out_key = final_out.buffer_key
+
+    slots: dict[str, int] = {}
+    for key in (src_a.buffer_key, src_b.buffer_key):
+        slots.setdefault(key, len(slots))
+    out_slot = len(slots)
+    base = out_slot + 1
+    extras = Extras(base_slots_by_key={**slots, out_key: out_slot})
+
+    helpers: list[str] = []
+    pro_a = pro_b = None
+    if decision.prologue_a:
+        pro_a = ChainCode(decision.prologue_a, (src_a.name,), "prologue_a")
+        pro_a.register_extras(extras, base)
+        helpers.append(pro_a.helper())
+    if decision.prologue_b:
+        pro_b = ChainCode(decision.prologue_b, (src_b.name,), "prologue_b")
+        pro_b.register_extras(extras, base)
+        helpers.append(pro_b.helper())
+    value_expr = None
+    if decision.epilogue:
+        epi = ChainCode(decision.epilogue, (anchor.out.name,), "epilogue")
+        epi.register_extras(extras, base)
+        helpers.append(epi.helper())
+        value_expr = epi.scalar_call(["{a0}"], "row", "col")
+
+    config = MatmulConfig(
+        tile=tile,
+        aligned=aligned,
+        M_dim_var="M",
+        K_dim_var="K",
+        N_dim_var="N",
+        a_buffer_name=param_name(src_a.buffer_key),
+        b_buffer_name=param_name(src_b.buffer_key),
+        c_buffer_name=param_name(out_key),
+        a_tile_name="A_tile",
+        b_tile_name="B_tile",
+    )
+    config.validate()
+    a_load = operand_load(name="load_A_tile", src=src_a, dst="A_tile", tile=tile, side="a",
+                          M=M, K=K, N=N, aligned=aligned, prologue=pro_a)
+    b_load = operand_load(name="load_B_tile", src=src_b, dst="B_tile", tile=tile, side="b",
+                          M=M, K=K, N=N, aligned=aligned, prologue=pro_b)
+    mainloop = MatmulMainloopFragment(
+        tile_K=tile.tile_K,
+        fragments=(a_load, b_load, BarrierFragment("inputs_ready"), MatmulComputeFragment(config),
+                   BarrierFragment("compute_done")),
+        K_dim_var="K",
+    )
+    store = MatmulEpilogueStoreFragment(config, value_expr=value_expr, check=not aligned)
+    fragments = (MatmulTileMappingFragment(), ThreadIndexFragment(tile), MatmulSetupFragment(config), mainloop, store)
+    ctx = CodegenContext(
+        function_name=function_name or f"matmul_{anchor.out.name}_fused",
+        buffers=(*(input_param(k) for k in slots), output_param(out_key), *extras.buffers),
+        dims=("M", "K", "N"),
+        tg_x=tile.tg_x,
+        tg_y=1,
+        threadgroup_decls=(lds_decl("A_tile", tile.a_tile_shape()), lds_decl("B_tile", tile.b_tile_shape())),
+        helpers=tuple(helpers),
+    )
+    return KernelGroup(
+        kernel=Kernel(fragments=fragments, ctx=ctx),
+        bindings=(*slots, out_key, *extras.bindings),
+        dims=(M, K, N),
+        grid=grid_for(M, N, tile),
+        threads=(tile.tg_x, 1, 1),
+        ops=decision.ops,
+        strategy=decision.strategy,
+    )

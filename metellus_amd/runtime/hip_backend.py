@@ -1,0 +1,260 @@
+"""ctypes wrapper over the native shim ``libmetellus_hip.so``.
+
+Exposes the seven functions of the reference's native module
+(reference: src/metal_backend.mm:253-261) with the same names, arguments
+and error behaviour (failures raise ``RuntimeError``):
+
+    create_buffer(nbytes) -> int          release_buffer(handle) -> bool
+    buffer_size(handle) -> int            write_buffer(handle, ndarray)
+    read_buffer(handle, ndarray)          fill_buffer(handle, value)
+    run_kernel(source, function_name, buffers, grid, threads, *, dims=(), dims_slot=None)
+        -> {"time_ms": float}
+
+plus the finer-grained ``compile_kernel`` / ``launch`` used by the runtime.
+
+The library is built in-tree by ``__graft_entry__.build()`` (hipcc, gfx950).
+There is no fallback: if the library or a GPU is missing, calls fail loudly.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import numpy as np
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_lib", "libmetellus_hip.so")
+
+# Symbols declared in include/metellus_hip.h (checked by the CPU test suite).
+EXPORTED_SYMBOLS = (
+    "mt_last_error",
+    "mt_init",
+    "mt_device_count",
+    "mt_device_info",
+    "mt_alloc",
+    "mt_free",
+    "mt_size",
+    "mt_device_ptr",
+    "mt_write",
+    "mt_read",
+    "mt_fill",
+    "mt_compile",
+    "mt_compile_only",
+    "mt_launch",
+    "mt_sync",
+    "mt_cache_stats",
+)
+
+_lib = None
+_lock = threading.Lock()
+
+_u64 = ctypes.c_uint64
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"native HIP shim not built: {_LIB_PATH} is missing "
+                "(run `python -c 'import __graft_entry__ as g; g.build()'` at the repo root)"
+            )
+        lib = ctypes.CDLL(_LIB_PATH)
+        sig = {
+            "mt_last_error": ([], ctypes.c_char_p),
+            "mt_init": ([], ctypes.c_int),
+            "mt_device_count": ([ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+            "mt_device_info": (
+                [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)],
+                ctypes.c_int,
+            ),
+            "mt_alloc": ([ctypes.c_size_t, ctypes.POINTER(_u64)], ctypes.c_int),
+            "mt_free": ([_u64, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+            "mt_size": ([_u64, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+            "mt_device_ptr": ([_u64, ctypes.POINTER(_u64)], ctypes.c_int),
+            "mt_write": ([_u64, ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int),
+            "mt_read": ([_u64, ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int),
+            "mt_fill": ([_u64, ctypes.c_uint8], ctypes.c_int),
+            "mt_compile": ([ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_u64)], ctypes.c_int),
+            "mt_compile_only": (
+                [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_size_t)],
+                ctypes.c_int,
+            ),
+            "mt_launch": (
+                [_u64, ctypes.POINTER(_u64), ctypes.c_int, _u32p, ctypes.c_int, ctypes.c_int, _u32p, _u32p,
+                 ctypes.c_int, ctypes.POINTER(ctypes.c_float)],
+                ctypes.c_int,
+            ),
+            "mt_sync": ([], ctypes.c_int),
+            "mt_cache_stats": ([ctypes.POINTER(_u64), ctypes.POINTER(_u64)], ctypes.c_int),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+        return lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        msg = _load().mt_last_error().decode("utf-8", "replace")
+        raise RuntimeError(msg)
+
+
+def library():
+    """The loaded ctypes library (raises if it was not built)."""
+    return _load()
+
+
+# ---------------------------------------------------------------------------
+# device
+# ---------------------------------------------------------------------------
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    _check(_load().mt_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def device_info() -> dict:
+    arch = ctypes.create_string_buffer(128)
+    cus = ctypes.c_int(0)
+    clk = ctypes.c_int(0)
+    _check(_load().mt_device_info(arch, 128, ctypes.byref(cus), ctypes.byref(clk)))
+    return {"arch": arch.value.decode(), "cu_count": cus.value, "clock_khz": clk.value}
+
+
+def synchronize() -> None:
+    _check(_load().mt_sync())
+
+
+def cache_stats() -> tuple[int, int]:
+    c, h = _u64(0), _u64(0)
+    _check(_load().mt_cache_stats(ctypes.byref(c), ctypes.byref(h)))
+    return c.value, h.value
+
+
+# ---------------------------------------------------------------------------
+# buffers (reference names)
+# ---------------------------------------------------------------------------
+
+
+def create_buffer(nbytes: int) -> int:
+    h = _u64(0)
+    _check(_load().mt_alloc(int(nbytes), ctypes.byref(h)))
+    return h.value
+
+
+def release_buffer(handle: int) -> bool:
+    existed = ctypes.c_int(0)
+    _check(_load().mt_free(int(handle), ctypes.byref(existed)))
+    return bool(existed.value)
+
+
+def buffer_size(handle: int) -> int:
+    n = ctypes.c_size_t(0)
+    _check(_load().mt_size(int(handle), ctypes.byref(n)))
+    return n.value
+
+
+def device_address(handle: int) -> int:
+    a = _u64(0)
+    _check(_load().mt_device_ptr(int(handle), ctypes.byref(a)))
+    return a.value
+
+
+def _handle_of(item) -> int:
+    if hasattr(item, "handle"):
+        return int(item.handle)
+    if isinstance(item, (int, np.integer)):
+        return int(item)
+    raise TypeError(f"expected a Buffer or an int handle; got {type(item).__name__}")
+
+
+def write_buffer(handle, data: np.ndarray) -> None:
+    arr = np.ascontiguousarray(data)
+    _check(_load().mt_write(_handle_of(handle), arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes))
+
+
+def read_buffer(handle, out: np.ndarray) -> None:
+    if not out.flags["C_CONTIGUOUS"]:
+        raise ValueError("read_buffer: destination must be C-contiguous")
+    _check(_load().mt_read(_handle_of(handle), out.ctypes.data_as(ctypes.c_void_p), out.nbytes))
+
+
+def fill_buffer(handle, value: int) -> None:
+    if not 0 <= int(value) <= 255:
+        raise ValueError(f"fill value must be in [0, 255]; got {value}")
+    _check(_load().mt_fill(_handle_of(handle), int(value)))
+
+
+# ---------------------------------------------------------------------------
+# kernels
+# ---------------------------------------------------------------------------
+
+
+def compile_kernel(source: str, function_name: str, options: str = "") -> int:
+    """hiprtc-compile (cached) and load; returns a kernel handle."""
+    k = _u64(0)
+    _check(_load().mt_compile(source.encode(), function_name.encode(), options.encode(), ctypes.byref(k)))
+    return k.value
+
+
+def compile_only(source: str, options: str = "", target: str = "gfx950") -> int:
+    """hiprtc-compile without a device; returns the code-object size."""
+    n = ctypes.c_size_t(0)
+    _check(_load().mt_compile_only(source.encode(), options.encode(), target.encode(), ctypes.byref(n)))
+    return n.value
+
+
+def launch(
+    kernel: int,
+    buffers,
+    dims,
+    dims_slot: int,
+    grid,
+    threads,
+    timed: bool = False,
+) -> float | None:
+    """Launch ``kernel``; buffers are handles (or objects with ``.handle``).
+    Returns the kernel time in ms when ``timed``."""
+    handles = [_handle_of(b) for b in buffers]
+    nb = len(handles)
+    bufs = (_u64 * max(nb, 1))(*handles)
+    dims_l = [int(d) for d in dims]
+    for d in dims_l:
+        if not 0 <= d < 2**32:
+            raise ValueError(f"dim value {d} does not fit in uint32")
+    dims_a = (ctypes.c_uint32 * max(len(dims_l), 1))(*dims_l)
+    grid_a = (ctypes.c_uint32 * 3)(*[int(g) for g in grid])
+    block_a = (ctypes.c_uint32 * 3)(*[int(t) for t in threads])
+    ms = ctypes.c_float(0.0)
+    _check(
+        _load().mt_launch(
+            kernel, bufs, nb, dims_a, len(dims_l), int(dims_slot), grid_a, block_a, 1 if timed else 0,
+            ctypes.byref(ms),
+        )
+    )
+    return float(ms.value) if timed else None
+
+
+def run_kernel(source: str, function_name: str, buffers, grid, threads, *, dims=(), dims_slot=None) -> dict:
+    """Compile (cached) + launch + wait, returning ``{"time_ms": t}`` like the
+    reference (reference: src/metal_backend.mm:178-249).  ``dims`` are passed
+    by value at ``dims_slot`` (default: after the buffers)."""
+    k = compile_kernel(source, function_name)
+    slot = len(buffers) if dims_slot is None else int(dims_slot)
+    t = launch(k, buffers, dims, slot, grid, threads, timed=True)
+    return {"time_ms": t}
