@@ -1,0 +1,414 @@
+"""Benchmark: fused-kernel fp32 TFLOP/s and HBM GB/s (% of roofline) on 1x MI355X.
+
+Headline workload (C2): the fused elementwise
+chain ``out = sigmoid(a*b + c) * d`` on four 4096x4096 fp32 tensors (N(0,1),
+seed 1) -- one kernel, 5 x 64 MiB of algorithmic HBM traffic per step.
+
+A *step* is one launch of the workload's fused kernel(s) on inputs already
+resident in HBM.  Before every timed step the 256 MiB Infinity Cache is
+flushed by reading a 512 MiB scratch buffer (outside the event bracket), so
+the bandwidth is HBM bandwidth.  Kernel durations come from HIP events
+recorded on the shim's stream around each launch.
+
+Also measured (``per_config``): C3 softmax (4 kernels), the 4096^3 matmul,
+C4 MLP block (literal 4-kernel partition and the fused diamond variant), C5
+attention heads (5 kernels per head), each kernel against its roofline.
+
+``cpu_baseline``: the CPU oracle (NumPy, single-threaded ufuncs) evaluating
+the same C2 expression on the same full-size inputs for ~10 s on the host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5]
+       [--no-extra] [--no-cpu] [--no-flush] [--repeat-kernel NAME --steps K] (profiling)
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+
+def _c2():
+    from tests.gpu_cases import sigmoid_chain
+
+    return sigmoid_chain(4096, 4096, seed=1)
+
+
+def _c3():
+    from tests.gpu_cases import softmax
+
+    return softmax(8192, 8192, seed=2)
+
+
+def _gemm():
+    from tests.gpu_cases import plain_matmul
+
+    return plain_matmul(4096, 4096, 4096, seed=0)
+
+
+def _c4(diamond=False):
+    from tests.gpu_cases import mlp_block
+
+    return mlp_block(4096, 4096, 11008, seed=3, diamond=diamond)
+
+
+def _c5(head=0):
+    from tests.gpu_cases import attention_head
+
+    return attention_head(2048, 128, seed=4, head=head, heads=32)
+
+
+# ---------------------------------------------------------------------------
+# per-kernel algorithmic work
+# ---------------------------------------------------------------------------
+
+
+def kernel_work(group, tensors) -> tuple[str, float]:
+    """('hbm', bytes) or ('mfma', flops) for one launch of ``group``:
+    every binding read once plus the output written once (elementwise,
+    reduction, copy); 2*M*N*K per anchor for matmul kernels."""
+    from metellus_amd.orchestrator.ir import MatmulOp
+
+    mm = [op for op in group.ops if isinstance(op, MatmulOp)]
+    if mm:
+        return "mfma", float(sum(2 * op.a.shape[0] * op.a.shape[1] * op.b.shape[1] for op in mm))
+    nbytes = 0
+    for key in group.bindings:
+        nbytes += tensors[key].nbytes
+    return "hbm", float(nbytes)
+
+
+class Prepared:
+    """A compiled program with device-resident inputs/outputs, ready for
+    repeated timed launches of its kernels."""
+
+    def __init__(self, ops):
+        from metellus_amd.api import compile_program
+        from metellus_amd.runtime import hip_backend
+        from metellus_amd.runtime.buffer import Buffer
+
+        self.ops = ops
+        self.groups = compile_program(ops)
+        self.tensors = ops.tensors
+        self.env = {}
+        nbytes = {op.out.buffer_key: op.out.nbytes for op in ops.build()}
+        for name, arr in ops.uploads.items():
+            self.env[name] = Buffer.from_numpy(arr)
+        for g in self.groups:
+            for k in g.bindings:
+                if k not in self.env:
+                    self.env[k] = Buffer(nbytes[k])
+            _ = g.kernel.handle  # hiprtc compile outside the timed region
+        self.hip = hip_backend
+        # a key -> Tensor map for byte counts (owners)
+        self.owner = {}
+        for t in self.tensors.values():
+            if t.buffer_key == t.name:
+                self.owner[t.name] = t
+
+    def launch(self, i, timed=False):
+        g = self.groups[i]
+        return self.hip.launch(
+            g.kernel.handle, [self.env[k] for k in g.bindings], g.dims, g.kernel.dims_slot_index,
+            g.grid, g.threads, timed=timed,
+        )
+
+    def run_all(self):
+        for i in range(len(self.groups)):
+            self.launch(i)
+
+    def download(self, key, shape):
+        return self.env[key].numpy(shape, np.float32)
+
+    def release(self):
+        for b in self.env.values():
+            b.release()
+        self.env.clear()
+
+
+class Flusher:
+    """Evicts the 256 MiB Infinity Cache by *reading* a 512 MiB buffer (a
+    row-sum kernel of this framework).  A write-based flush (memset) would
+    leave dirty lines whose write-back then lands inside the measured
+    kernel; after a read flush the cache holds only clean lines."""
+
+    ROWS, COLS = 16384, 8192  # 512 MiB of fp32
+
+    def __init__(self):
+        from metellus_amd.api import compile_program
+        from metellus_amd.orchestrator import Operations
+        from metellus_amd.runtime import hip_backend
+        from metellus_amd.runtime.buffer import Buffer
+
+        ops = Operations()
+        ops.input("flush_src", (self.ROWS, self.COLS))
+        ops.reduction("sum", out="flush_sum", x="flush_src")
+        (self.group,) = compile_program(ops)
+        self.src = Buffer(self.ROWS * self.COLS * 4)
+        self.src.fill(0)
+        self.dst = Buffer(self.ROWS * 4)
+        self.hip = hip_backend
+
+    def flush(self):
+        g = self.group
+        self.hip.launch(g.kernel.handle, [self.src, self.dst], g.dims, g.kernel.dims_slot_index, g.grid, g.threads)
+
+    def release(self):
+        self.src.release()
+        self.dst.release()
+
+
+def time_kernels(prep: Prepared, steps: int, warmup: int, flusher, label: str) -> list[dict]:
+    """Per kernel: warm up, then ``steps`` event-timed launches, each after
+    an Infinity Cache flush (when ``flusher`` is given)."""
+    out = []
+    for i, g in enumerate(prep.groups):
+        for _ in range(warmup):
+            prep.launch(i)
+        prep.hip.synchronize()
+        ms = []
+        for s in range(steps):
+            if flusher is not None:
+                flusher.flush()
+            ms.append(prep.launch(i, timed=True))
+        bound, work = kernel_work(g, prep.owner)
+        mean = float(np.mean(ms))
+        if bound == "hbm":
+            achieved = work / (mean * 1e-3) / 1e9
+            peak, unit = HBM_PEAK_GBS, "GB/s"
+        else:
+            achieved = work / (mean * 1e-3) / 1e12
+            peak, unit = FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
+        out.append(
+            {
+                "kernel": g.kernel.function_name,
+                "config": label,
+                "strategy": g.strategy.value,
+                "grid": list(g.grid),
+                "threads": list(g.threads),
+                "ms_mean": round(mean, 5),
+                "ms_min": round(float(np.min(ms)), 5),
+                "ms_median": round(float(np.median(ms)), 5),
+                "bound": bound,
+                "work": work,
+                "achieved": round(achieved, 2),
+                "peak": peak,
+                "unit": unit,
+                "frac": round(achieved / peak, 4),
+            }
+        )
+        log(f"[bench] {label} {g.kernel.function_name}: {mean:.4f} ms  {achieved:.1f} {unit} ({100*achieved/peak:.1f}%)")
+    return out
+
+
+def check_c2(prep: Prepared) -> float:
+    """Max abs error of the GPU output on 64 sampled rows vs the oracle."""
+    from oracle.ir_eval import apply_elementwise
+
+    out = prep.download("out", (4096, 4096))
+    rows = np.random.default_rng(0).choice(4096, 64, replace=False)
+    u = {k: prep.ops.uploads[k][rows] for k in "abcd"}
+    t = apply_elementwise("mul", u["a"], u["b"])
+    t = apply_elementwise("add", t, u["c"])
+    t = apply_elementwise("negate", t)
+    t = apply_elementwise("exp", t)
+    t = apply_elementwise("add", t, np.float32(1.0))
+    t = apply_elementwise("recip", t)
+    t = apply_elementwise("mul", t, u["d"])
+    err = np.abs(out[rows] - t)
+    tol = 1e-5 + 1e-5 * np.abs(t)
+    if not np.all(err <= tol):
+        raise AssertionError(f"C2 output mismatch: max err {err.max():.3e}")
+    return float(err.max())
+
+
+def cpu_baseline_c2(ops, budget_s: float = 10.0) -> dict:
+    """Time the CPU oracle on the full C2 inputs for about ``budget_s``."""
+    from oracle.ir_eval import apply_elementwise
+
+    a, b, c, d = (ops.uploads[k] for k in "abcd")
+
+    def once():
+        t = apply_elementwise("mul", a, b)
+        t = apply_elementwise("add", t, c)
+        t = apply_elementwise("negate", t)
+        t = apply_elementwise("exp", t)
+        t = apply_elementwise("add", t, np.float32(1.0))
+        t = apply_elementwise("recip", t)
+        return apply_elementwise("mul", t, d)
+
+    once()
+    n, t0 = 0, time.perf_counter()
+    times = []
+    while time.perf_counter() - t0 < budget_s or n < 3:
+        s = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - s)
+        n += 1
+    med = float(np.median(times))
+    return {
+        "value": round(335_544_320 / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"full C2 inputs (4 x 4096x4096 fp32), oracle/ir_eval.py NumPy ufuncs, {n} evaluations, median {med*1e3:.1f} ms",
+    }
+
+
+def read_profile_traffic(name: str) -> float | None:
+    """HBM bytes per launch of the C2 kernel from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated)."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    with open(path, encoding="utf-8") as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                try:
+                    return float(line.split(":", 1)[1].strip())
+                except ValueError:
+                    return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default=None)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-flush", action="store_true")
+    ap.add_argument("--c5-heads", type=int, default=4)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            "bench.py: this build measures one MI355X; the path shards by rows / heads / output "
+            "tiles with no exchange (see DESIGN.md), and multi-GPU runs are not part of it. "
+            f"Requested --gpus {args.gpus} (WORLD_SIZE={world}).",
+            file=sys.stderr,
+        )
+        return 2
+
+    from metellus_amd.runtime import hip_backend
+    info = hip_backend.device_info()
+    log(f"[bench] device {info}")
+    flush = None if args.no_flush else Flusher()
+
+    # ---- headline: C2 ------------------------------------------------------
+    only = args.only
+    line = None
+    per_config: list[dict] = []
+    if only in (None, "c2"):
+        log("[bench] C2 sigmoid chain 4096x4096: preparing")
+        prep = time_prep = Prepared(_c2())
+        assert len(prep.groups) == 1
+        for _ in range(args.warmup):
+            prep.launch(0)
+        hip_backend.synchronize()
+        kernel_ms = []
+        t0 = time.perf_counter()
+        for s in range(args.steps):
+            if flush is not None:
+                flush.flush()
+            kernel_ms.append(prep.launch(0, timed=True))
+        hip_backend.synchronize()
+        wall = time.perf_counter() - t0
+        err = check_c2(prep)
+        ms = float(np.mean(kernel_ms))
+        bytes_per_step = 335_544_320
+        gbs = bytes_per_step / (ms * 1e-3) / 1e9
+        traffic = read_profile_traffic("elementwise_out_fused_c2_pmc.txt")
+        g = prep.groups[0]
+        line = {
+            "metric": "fused-kernel fp32 TFLOP/s & HBM GB/s (% of roofline), 1×MI355X",
+            "value": round(gbs, 2),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms, 5),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "f32",
+            "data": "synthetic (N(0,1), numpy seed 1)",
+            "config": {
+                "workload": "C2: out = sigmoid(a*b + c) * d, 4 fp32 inputs 4096x4096, one fused kernel",
+                "kernel": g.kernel.function_name,
+                "strategy": g.strategy.value,
+                "grid": list(g.grid),
+                "threads": list(g.threads),
+                "bytes_per_step": bytes_per_step,
+                "cache_flush_between_steps": flush is not None,
+                "wall_ms_per_step_incl_flush": round(wall * 1e3 / args.steps, 4),
+                "max_abs_err_vs_oracle_sampled_rows": err,
+                "device": info["arch"],
+                "parallelism": "1 GPU",
+            },
+            "roofline": {
+                "bound": "hbm",
+                "achieved": round(gbs, 2),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": traffic,
+            },
+        }
+        log(f"[bench] C2: {ms:.4f} ms/step, {gbs:.1f} GB/s ({100*gbs/HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+        if not args.no_cpu:
+            log("[bench] CPU baseline (oracle, ~10 s)")
+            line["cpu_baseline"] = cpu_baseline_c2(prep.ops)
+        prep.release()
+        del time_prep
+
+    # ---- other configs -----------------------------------------------------
+    if not args.no_extra or only not in (None, "c2"):
+        extra_steps = max(3, min(args.steps, 10))
+        todo = []
+        if only in (None, "c3"):
+            todo.append(("C3 softmax 8192x8192", _c3))
+        if only in (None, "gemm"):
+            todo.append(("matmul 4096^3", _gemm))
+        if only in (None, "c4"):
+            todo.append(("C4 MLP literal", lambda: _c4(False)))
+            todo.append(("C4 MLP diamond", lambda: _c4(True)))
+        if only in (None, "c5"):
+            for h in range(args.c5_heads):
+                todo.append((f"C5 attention head {h}", lambda h=h: _c5(h)))
+        for label, make in todo:
+            log(f"[bench] {label}: preparing")
+            prep = Prepared(make())
+            per_config += time_kernels(prep, extra_steps, 2, flush, label)
+            prep.release()
+    if line is None:
+        line = {"metric": "fused-kernel fp32 TFLOP/s & HBM GB/s (% of roofline), 1×MI355X", "value": None}
+    line["per_kernel"] = per_config
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -29,12 +29,22 @@ from dataclasses import dataclass, field
 
 from metellus_amd.compute.elementwise.elementwise import BroadcastSpec
 from metellus_amd.compute.fragments import CodegenContext, TgmemAccess
-from metellus_amd.orchestrator.assembly.expressions import ChainCode, External
-from metellus_amd.orchestrator.assembly.extras import param_name
+from metellus_amd.compute.elementwise.chain import ChainCode, External, param_name
 from metellus_amd.orchestrator.ir import Tensor
 
 NWAVES = 4
 NT = 64 * NWAVES
+
+# Streaming policy, chosen by measurement on MI355X with the Infinity Cache
+# flushed (C2 chain 4096^2, C3 chains 8192^2): nontemporal 128-bit loads,
+# ordinary stores; flat: 1024 lanes x 1 float4 per lane (~6.1 TB/s; the
+# 256-1024 lane, 1-4 float4 variants all land within 5.9-6.1 TB/s); tiled:
+# 8 elements per lane (~6.8 TB/s).
+FLAT_THREADS = 1024
+FLAT_UNROLL = 1
+TILED_ELEMS = 8  # elements per lane in the tiled layout
+NT_LOAD = True
+NT_STORE = False
 
 
 def _ceil_div(a: int, b: int) -> int:
@@ -54,6 +64,9 @@ class StreamLayout:
     vec: int = 4
     unroll: int = 4  # flat: float4 per lane; tiled: rows per lane (RPW)
     lpr: int = 64  # tiled: lanes per row
+    threads: int = NT  # lanes per workgroup (flat layout)
+    nt_load: bool = NT_LOAD  # nontemporal (streaming) loads
+    nt_store: bool = NT_STORE  # nontemporal stores
 
     def tile(self) -> tuple[int, int]:
         """(TM, TN) of one workgroup for the tiled layout."""
@@ -70,17 +83,20 @@ def choose_layout(primary: Tensor, externals: list[External], M: int, N: int) ->
         for e in externals
     )
     if flat:
-        return StreamLayout("flat", vec=4, unroll=4)
+        assert FLAT_THREADS % 64 == 0 and FLAT_THREADS <= 1024
+        return StreamLayout(
+            "flat", vec=4, unroll=FLAT_UNROLL, threads=FLAT_THREADS, nt_load=NT_LOAD, nt_store=NT_STORE
+        )
     vec = 4 if N % 4 == 0 else 1
     lpr = min(64, _next_pow2(_ceil_div(N, vec)))
     rows_per_step = NWAVES * (64 // lpr)
-    rpw = max(1, min(16 // vec, _ceil_div(M, rows_per_step)))
-    return StreamLayout("tiled", vec=vec, unroll=rpw, lpr=lpr)
+    rpw = max(1, min(max(1, TILED_ELEMS // vec), _ceil_div(M, rows_per_step)))
+    return StreamLayout("tiled", vec=vec, unroll=rpw, lpr=lpr, nt_load=NT_LOAD, nt_store=NT_STORE)
 
 
 def grid_for_layout(layout: StreamLayout, M: int, N: int) -> tuple[int, int, int]:
     if layout.kind == "flat":
-        return (_ceil_div(M * N, NT * 4 * layout.unroll), 1, 1)
+        return (_ceil_div(M * N, layout.threads * 4 * layout.unroll), 1, 1)
     tm, tn = layout.tile()
     return (_ceil_div(N, tn), _ceil_div(M, tm), 1)
 
@@ -115,6 +131,12 @@ class ElementwiseStreamFragment:
     def _operands(self) -> list[External]:
         return [External(self.primary, BroadcastSpec.NONE), *self.code.externals]
 
+    def _ld4(self, addr: str) -> str:
+        return f"mt_ld4_nt({addr})" if self.layout.nt_load else f"mt_ld4({addr})"
+
+    def _st4(self, addr: str, val: str) -> str:
+        return f"mt_st4_nt({addr}, {val})" if self.layout.nt_store else f"mt_st4({addr}, {val})"
+
     def render(self, ctx: CodegenContext) -> str:
         if self.layout.kind == "flat":
             return self._render_flat()
@@ -122,11 +144,12 @@ class ElementwiseStreamFragment:
 
     def _render_flat(self) -> str:
         U = self.layout.unroll
+        T = self.layout.threads
         out = param_name(self.out_key)
         ops = self._operands()
         lines = [
             "const size_t E = (size_t)M * (size_t)N;",
-            f"const size_t base = (size_t)blockIdx.x * {NT * 4 * U}u + (size_t)threadIdx.x * 4u;",
+            f"const size_t base = (size_t)blockIdx.x * {T * 4 * U}u + (size_t)threadIdx.x * 4u;",
         ]
         regs = []
         for k, e in enumerate(ops):
@@ -139,22 +162,22 @@ class ElementwiseStreamFragment:
                 regs.append(("vec", f"r{k}", p))
         lines.append("#pragma unroll")
         lines.append(f"for (int u = 0; u < {U}; ++u) {{")
-        lines.append(f"    const size_t idx = base + (size_t)u * {NT * 4}u;")
+        lines.append(f"    const size_t idx = base + (size_t)u * {T * 4}u;")
         lines.append("    if (idx + 4u <= E) {")
         for kind, r, p in regs:
             if kind == "vec":
-                lines.append(f"        {r}[u] = mt_ld4({p} + idx);")
+                lines.append(f"        {r}[u] = {self._ld4(f'{p} + idx')};")
         lines.append("    }")
         lines.append("}")
         lines.append("#pragma unroll")
         lines.append(f"for (int u = 0; u < {U}; ++u) {{")
-        lines.append(f"    const size_t idx = base + (size_t)u * {NT * 4}u;")
+        lines.append(f"    const size_t idx = base + (size_t)u * {T * 4}u;")
         lines.append("    if (idx + 4u <= E) {")
         lines.append("        mt_f32x4 o;")
         for j in range(4):
             vals = [f"{r}[u][{j}]" if kind == "vec" else r for kind, r, _ in regs]
             lines.append(f"        o[{j}] = {self.code.call(vals[:1], vals[1:])};")
-        lines.append(f"        mt_st4({out} + idx, o);")
+        lines.append(f"        {self._st4(f'{out} + idx', 'o')};")
         lines.append("    } else {")
         lines.append("        for (size_t i = idx; i < E; ++i) {")
         vals = [f"{p}[i]" if kind == "vec" else r for kind, r, p in regs]
@@ -197,7 +220,8 @@ class ElementwiseStreamFragment:
             p = param_name(e.tensor.buffer_key)
             if kinds[k] == "vec":
                 if _vector_ok(e.tensor, e.broadcast):
-                    lines.append(f"        r{k}[k] = mt_ld4({p} + {e.offset('row', 'col')});")
+                    addr = p + " + " + e.offset("row", "col")
+                    lines.append(f"        r{k}[k] = {self._ld4(addr)};")
                 else:
                     comps = ", ".join(f"{p}[{e.offset('row', f'col + {j}u')}]" for j in range(4))
                     lines.append(f"        r{k}[k] = mt_f32x4{{{comps}}};")
@@ -214,7 +238,7 @@ class ElementwiseStreamFragment:
             for j in range(4):
                 vals = [f"r{k}[k][{j}]" if kinds[k] == "vec" else f"r{k}[k]" for k in range(len(ops))]
                 lines.append(f"        o[{j}] = {self.code.call(vals[:1], vals[1:])};")
-            lines.append(f"        mt_st4({out} + (size_t)row * N + col, o);")
+            lines.append(f"        {self._st4(f'{out} + (size_t)row * N + col', 'o')};")
         else:
             vals = [f"r{k}[k]" for k in range(len(ops))]
             lines.append(f"        {out}[(size_t)row * N + col] = {self.code.call(vals[:1], vals[1:])};")

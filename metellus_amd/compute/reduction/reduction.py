@@ -34,7 +34,10 @@ REDUCTION_OPS = ("sum", "max", "min", "product")
 
 ValueTransform = Callable[[str], str]
 
-UNROLL = 4
+# Measured on MI355X (8192^2 rows, cache flushed): 16 float4 in flight per
+# lane with ordinary loads reads at ~6.9 TB/s.
+UNROLL = 16  # float4 chunks (or elements) in flight per lane
+NT_LOAD = False  # nontemporal (streaming) row loads
 
 
 def _identity(op: str) -> str:
@@ -110,6 +113,8 @@ class LastAxisReductionComputeFragment:
     waves_per_row: int | None = None
     rows_per_group: int = 1
     vectorized: bool | None = None
+    unroll: int = UNROLL
+    nt_load: bool = NT_LOAD
     kind: str = "compute"
 
     @property
@@ -131,6 +136,8 @@ class LastAxisReductionComputeFragment:
     def render(self, ctx: CodegenContext) -> str:
         _check_op(self.op)
         W, T = self.W, 64 * self.W
+        U = self.unroll
+        ld4 = "mt_ld4_nt" if self.nt_load else "mt_ld4"
         ident = _identity(self.op)
         tf = self.value_transform or (lambda raw: raw)
         src = f"{self.input_name} + (size_t)row * {self.row_stride}u"
@@ -140,12 +147,12 @@ class LastAxisReductionComputeFragment:
             L += [
                 f"    const unsigned nq = {self.reduce_dim} / 4u;",
                 "    unsigned q = t;",
-                f"    for (; q + {(UNROLL - 1) * T}u < nq; q += {UNROLL * T}u) {{",
-                f"        mt_f32x4 x[{UNROLL}];",
+                f"    for (; q + {(U - 1) * T}u < nq; q += {U * T}u) {{",
+                f"        mt_f32x4 x[{U}];",
                 "#pragma unroll",
-                f"        for (int u = 0; u < {UNROLL}; ++u) x[u] = mt_ld4(src + 4u * (q + (unsigned)u * {T}u));",
+                f"        for (int u = 0; u < {U}; ++u) x[u] = {ld4}(src + 4u * (q + (unsigned)u * {T}u));",
                 "#pragma unroll",
-                f"        for (int u = 0; u < {UNROLL}; ++u) {{",
+                f"        for (int u = 0; u < {U}; ++u) {{",
             ]
             for j in range(4):
                 L += [
@@ -156,7 +163,7 @@ class LastAxisReductionComputeFragment:
                 "        }",
                 "    }",
                 f"    for (; q < nq; q += {T}u) {{",
-                "        const mt_f32x4 xv = mt_ld4(src + 4u * q);",
+                f"        const mt_f32x4 xv = {ld4}(src + 4u * q);",
             ]
             for j in range(4):
                 L += [
@@ -169,12 +176,12 @@ class LastAxisReductionComputeFragment:
             load = "src[idx]" if cs == "1" else f"src[(size_t)idx * {cs}u]"
             L += [
                 "    unsigned e = t;",
-                f"    for (; e + {(UNROLL - 1) * T}u < {self.reduce_dim}; e += {UNROLL * T}u) {{",
-                f"        float x[{UNROLL}];",
+                f"    for (; e + {(U - 1) * T}u < {self.reduce_dim}; e += {U * T}u) {{",
+                f"        float x[{U}];",
                 "#pragma unroll",
-                f"        for (int u = 0; u < {UNROLL}; ++u) {{ const unsigned idx = e + (unsigned)u * {T}u; x[u] = {load}; }}",
+                f"        for (int u = 0; u < {U}; ++u) {{ const unsigned idx = e + (unsigned)u * {T}u; x[u] = {load}; }}",
                 "#pragma unroll",
-                f"        for (int u = 0; u < {UNROLL}; ++u) {{",
+                f"        for (int u = 0; u < {U}; ++u) {{",
                 f"            const unsigned idx = e + (unsigned)u * {T}u; (void)idx;",
                 f"            a0 = {_combine(self.op, 'a0', tf('x[u]'))};",
                 "        }",

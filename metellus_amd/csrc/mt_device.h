@@ -35,6 +35,11 @@ struct mt_dims {
 
 MT_INLINE mt_f32x4 mt_ld4(const float* p) { return *reinterpret_cast<const mt_f32x4*>(p); }
 MT_INLINE void mt_st4(float* p, mt_f32x4 v) { *reinterpret_cast<mt_f32x4*>(p) = v; }
+// Streaming variants: nontemporal hint (data used once; do not keep in cache).
+MT_INLINE mt_f32x4 mt_ld4_nt(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const mt_f32x4*>(p));
+}
+MT_INLINE void mt_st4_nt(float* p, mt_f32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<mt_f32x4*>(p)); }
 
 MT_INLINE unsigned mt_lane() { return threadIdx.x & 63u; }
 // Wave index as a scalar (wave-uniform) value.

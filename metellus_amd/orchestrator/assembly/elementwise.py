@@ -8,7 +8,6 @@ Bindings ``(primary, out, *extras)`` and dims ``(M, N)`` (a 1-D primary is
 from __future__ import annotations
 
 from metellus_amd.compute.elementwise.stream import (
-    NT,
     ElementwiseStreamFragment,
     choose_layout,
     grid_for_layout,
@@ -38,7 +37,7 @@ def assemble_elementwise(decision: DecisionView, function_name: str | None) -> K
         function_name=function_name or f"elementwise_{final_out.name}_fused",
         buffers=(input_param(primary.buffer_key), output_param(final_out.buffer_key), *extras.buffers),
         dims=("M", "N"),
-        tg_x=NT,
+        tg_x=layout.threads,
         tg_y=1,
         helpers=(code.helper(),),
     )
@@ -47,7 +46,7 @@ def assemble_elementwise(decision: DecisionView, function_name: str | None) -> K
         bindings=(primary.buffer_key, final_out.buffer_key, *extras.bindings),
         dims=(M, N),
         grid=grid_for_layout(layout, M, N),
-        threads=(NT, 1, 1),
+        threads=(layout.threads, 1, 1),
         ops=decision.ops,
         strategy=decision.strategy,
     )

@@ -1,187 +1,19 @@
-"""Compile fused elementwise chains into HIP device code.
-
-A chain is a tuple of ``ElementwiseOp``s where each op's primary is the
-previous op's output (the first op's primary is the chain *seed*).  Secondary
-operands are Scalars (inlined literals), values computed earlier in the
-chain (registers), or *external* tensors read from global memory.
-
-``ChainCode`` turns a chain into one ``__device__`` helper
-
-    float <name>(float x, float e0, float e1, ...) { float v0 = ...; ...; return vN; }
-
-whose parameters are the seed value and one value per external operand; the
-calling template decides how the externals are fetched (128-bit vectors in
-streaming kernels, scalar loads in matmul prologues, ...).  Per-op expression
-text follows the reference's chain emission (reference:
-src/compute/elementwise/tiled_chain.py:65-79, src/orchestrator/assembly/
-expressions.py:33-170): ``float v{i} = <template with x/y/cond substituted>``,
-comparison results wrapped to 1.0f/0.0f.
-"""
+"""Chain expression helpers for the assembly templates (reference:
+src/orchestrator/assembly/expressions.py:1-205).  The chain compiler itself
+lives in ``compute.elementwise.chain``; this module keeps the reference's
+closure-style entry points on top of it."""
 
 from __future__ import annotations
 
-import math
-from dataclasses import dataclass, field
-
-from metellus_amd.compute.elementwise.elementwise import (
-    BroadcastSpec,
-    elementwise_arity,
-    elementwise_expression,
-    elementwise_outputs_bool,
-    substitute_placeholders,
+from metellus_amd.compute.elementwise.chain import (  # noqa: F401
+    ChainCode,
+    External,
+    scalar_literal,
+    substitute,
+    wrap_bool,
 )
-from metellus_amd.orchestrator.assembly.extras import Extras, param_name
-from metellus_amd.orchestrator.ir import ElementwiseOp, Scalar, Tensor
-
-
-def substitute(expr: str, **subs: str) -> str:
-    return substitute_placeholders(expr, **subs)
-
-
-def wrap_bool(op: str, expr: str) -> str:
-    if elementwise_outputs_bool(op):
-        return f"(({expr}) ? 1.0f : 0.0f)"
-    return expr
-
-
-def scalar_literal(value: float) -> str:
-    """fp32 literal (``f`` suffix); inf/nan become ``INFINITY``/``NAN``."""
-    if math.isnan(value):
-        return "NAN"
-    if math.isinf(value):
-        return "INFINITY" if value > 0 else "(-INFINITY)"
-    text = repr(float(value))
-    return f"{text}f"
-
-
-@dataclass(frozen=True)
-class External:
-    """A tensor operand of the chain read from global memory."""
-
-    tensor: Tensor
-    broadcast: BroadcastSpec
-
-    @property
-    def key(self) -> tuple:
-        t = self.tensor
-        return (t.buffer_key, t.row_stride, t.col_stride, self.broadcast)
-
-    def offset(self, row: str, col: str) -> str:
-        """Element offset of this operand at output position (row, col)."""
-        t = self.tensor
-        if self.broadcast is BroadcastSpec.SCALAR:
-            return "0"
-        if self.broadcast is BroadcastSpec.ROW:
-            return _term(col, t.col_stride) if len(t.shape) == 2 else _term(col, t.row_stride)
-        if self.broadcast is BroadcastSpec.COL:
-            return _term(row, t.row_stride)
-        if len(t.shape) == 1:
-            return _term(row, t.row_stride)
-        return _sum(_term(row, t.row_stride), _term(col, t.col_stride))
-
-    def scalar_fetch(self, row: str, col: str) -> str:
-        return f"{param_name(self.tensor.buffer_key)}[{self.offset(row, col)}]"
-
-
-def _term(var: str, stride: int) -> str:
-    if stride == 0:
-        return "0"
-    if stride == 1:
-        return f"(size_t)({var})"
-    return f"(size_t)({var}) * {stride}u"
-
-
-def _sum(a: str, b: str) -> str:
-    if a == "0":
-        return b
-    if b == "0":
-        return a
-    return f"{a} + {b}"
-
-
-@dataclass
-class ChainCode:
-    """Device helper for ``chain`` with ``seeds`` (names bound to the helper's
-    leading parameters, in order) already in registers."""
-
-    chain: tuple[ElementwiseOp, ...]
-    seeds: tuple[str, ...]
-    name: str
-    externals: list[External] = field(default_factory=list)
-
-    def __post_init__(self) -> None:
-        avail = set(self.seeds)
-        seen: dict[tuple, int] = {}
-        self._operand_ext: dict[tuple[int, int], int] = {}
-        for i, op in enumerate(self.chain):
-            for pos in range(1, elementwise_arity(op.op)):
-                o = op.operands[pos]
-                if isinstance(o, Tensor) and o.name not in avail:
-                    bc = op.y_broadcast if pos == 1 else op.cond_broadcast
-                    ext = External(o, bc)
-                    if ext.key not in seen:
-                        seen[ext.key] = len(self.externals)
-                        self.externals.append(ext)
-                    self._operand_ext[(i, pos)] = seen[ext.key]
-            avail.add(op.out.name)
-
-    def register_extras(self, extras: Extras, base_slot: int) -> None:
-        """Add external operands to the kernel's extra buffers, in the
-        reference's first-appearance order."""
-        for i, op in enumerate(self.chain):
-            for pos in range(1, elementwise_arity(op.op)):
-                if (i, pos) in self._operand_ext:
-                    extras.add_tensor(op.operands[pos], base_slot)
-
-    @property
-    def arity(self) -> int:
-        return len(self.seeds) + len(self.externals)
-
-    def helper(self) -> str:
-        params = [f"float s{k}" for k in range(len(self.seeds))]
-        params += [f"float e{k}" for k in range(len(self.externals))]
-        local: dict[str, str] = {name: f"s{k}" for k, name in enumerate(self.seeds)}
-        lines = []
-        cur = f"s0" if self.seeds else None
-        for i, op in enumerate(self.chain):
-            head = op.operands[0]
-            x = local.get(head.name, cur) if isinstance(head, Tensor) else cur
-            subs = {"x": f"({x})"}
-            for pos, ph in ((1, "y"), (2, "cond")):
-                if pos >= elementwise_arity(op.op):
-                    continue
-                o = op.operands[pos]
-                if isinstance(o, Scalar):
-                    subs[ph] = f"({scalar_literal(o.value)})"
-                elif (i, pos) in self._operand_ext:
-                    subs[ph] = f"(e{self._operand_ext[(i, pos)]})"
-                else:
-                    subs[ph] = f"({local[o.name]})"
-            expr = wrap_bool(op.op, substitute(elementwise_expression(op.op), **subs))
-            lines.append(f"    const float v{i} = {expr};")
-            cur = f"v{i}"
-            local[op.out.name] = cur
-        body = "\n".join(lines)
-        result = cur if cur is not None else "0.0f"
-        return (
-            f"__device__ __forceinline__ float {self.name}({', '.join(params)}) {{\n"
-            f"{body}\n    return {result};\n}}"
-        )
-
-    def call(self, seed_values: list[str], ext_values: list[str]) -> str:
-        return f"{self.name}({', '.join([*seed_values, *ext_values])})"
-
-    def scalar_call(self, seed_values: list[str], row: str, col: str) -> str:
-        """Call with every external fetched by a scalar load at (row, col)."""
-        return self.call(seed_values, [e.scalar_fetch(row, col) for e in self.externals])
-
-    def lambda_transform(self, row: str = "global_row", col: str = "global_col") -> str:
-        """``[=](float raw, unsigned row, unsigned col) -> float`` applying the
-        chain to a loaded element (matmul / reduction prologues)."""
-        return (
-            f"[=](float raw, unsigned {row}, unsigned {col}) -> float "
-            f"{{ return {self.scalar_call(['raw'], row, col)}; }}"
-        )
+from metellus_amd.orchestrator.assembly.extras import Extras
+from metellus_amd.orchestrator.ir import ElementwiseOp
 
 
 def chain_value_transform(chain, *, row_var, col_var, extras: Extras, base_slot: int, name: str = "chain"):

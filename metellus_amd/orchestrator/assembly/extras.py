@@ -14,12 +14,7 @@ from dataclasses import dataclass, field
 from metellus_amd.orchestrator.ir import Tensor
 
 
-def param_name(buffer_key: str) -> str:
-    """Kernel-parameter identifier for a buffer.  Prefixed so user tensor
-    names can never collide with the generated locals (``M``, ``row``...)."""
-    if buffer_key.isidentifier() and buffer_key.isascii():
-        return f"g_{buffer_key}"
-    return "g_x" + buffer_key.encode().hex()
+from metellus_amd.compute.elementwise.chain import param_name  # noqa: E402
 
 
 def input_param(buffer_key: str) -> str:

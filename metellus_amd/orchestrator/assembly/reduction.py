@@ -9,6 +9,7 @@ waves per row (see ``compute.reduction.reduction``); grid ``(ceil(M/R), 1, 1)``.
 from __future__ import annotations
 
 from metellus_amd.compute.fragments import CodegenContext, lds_decl
+from metellus_amd.compute.reduction import reduction as _red
 from metellus_amd.compute.reduction.reduction import (
     LastAxisReductionComputeFragment,
     LastAxisReductionSetupFragment,
@@ -26,11 +27,14 @@ from metellus_amd.orchestrator.kernel_group import KernelGroup
 from metellus_amd.runtime.program import Kernel
 
 WG_LANES = 256
+FORCE_WAVES_PER_ROW: int | None = None  # tuning override
 
 
 def reduction_waves_per_row(M: int, K: int) -> int:
     """Waves cooperating on one row: 1 when M rows already give >= 2048
     waves; otherwise up to 4, as long as each lane still gets >= 16 elements."""
+    if FORCE_WAVES_PER_ROW is not None:
+        return FORCE_WAVES_PER_ROW
     W = 1
     while W < 4 and M * W < 2048 and K >= 64 * (2 * W) * 16:
         W *= 2
@@ -74,6 +78,8 @@ def assemble_reduction(decision: DecisionView, function_name: str | None) -> Ker
         waves_per_row=W,
         rows_per_group=R,
         vectorized=vec,
+        unroll=_red.UNROLL,
+        nt_load=_red.NT_LOAD,
     )
     store = StoreReductionResultFragment(
         output_name=param_name(final_out.buffer_key),
@@ -108,4 +114,4 @@ def reduction_order(group: KernelGroup) -> dict:
     """The combine-order parameters of a reduction kernel (for the CPU
     replay of its exact order): op, waves per row, vector path."""
     frag = next(f for f in group.kernel.fragments if isinstance(f, LastAxisReductionComputeFragment))
-    return {"op": frag.op, "waves_per_row": frag.W, "vectorized": frag._vec(), "unroll": 4}
+    return {"op": frag.op, "waves_per_row": frag.W, "vectorized": frag._vec(), "unroll": frag.unroll}
