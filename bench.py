@@ -300,6 +300,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-flush", action="store_true")
     ap.add_argument("--c5-heads", type=int, default=4)
+    ap.add_argument(
+        "--calibrate-copy",
+        action="store_true",
+        help="also launch a plain 64 MiB -> 64 MiB copy kernel (for scaling PMC byte counters)",
+    )
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -384,8 +389,19 @@ def main() -> int:
         prep.release()
         del time_prep
 
+    if args.calibrate_copy:
+        log("[bench] copy calibration: 64 MiB in, 64 MiB out")
+        from metellus_amd.orchestrator import Operations
+
+        ops = Operations()
+        ops.from_numpy(np.random.default_rng(0).standard_normal((4096, 4096)).astype(np.float32), "cx")
+        ops.elementwise("mul", out="copyout", operands=("cx", 1.0))
+        prep = Prepared(ops)
+        per_config += time_kernels(prep, args.steps, 2, flush, "copy calibration 64 MiB")
+        prep.release()
+
     # ---- other configs -----------------------------------------------------
-    if not args.no_extra or only not in (None, "c2"):
+    if not args.no_extra and only is None or only not in (None, "c2"):
         extra_steps = max(3, min(args.steps, 10))
         todo = []
         if only in (None, "c3"):
