@@ -10,9 +10,10 @@ flushed by reading a 512 MiB scratch buffer (outside the event bracket), so
 the bandwidth is HBM bandwidth.  Kernel durations come from HIP events
 recorded on the shim's stream around each launch.
 
-Also measured (``per_config``): C3 softmax (4 kernels), the 4096^3 matmul,
+Also measured (``per_kernel``): C3 softmax (4 kernels), the 4096^3 matmul,
 C4 MLP block (literal 4-kernel partition and the fused diamond variant), C5
-attention heads (5 kernels per head), each kernel against its roofline.
+attention (32 heads; each of the 5 per-head kernels launched once for all
+heads, ``api.run_batch``), each kernel against its roofline.
 
 ``cpu_baseline``: the CPU oracle (NumPy, single-threaded ufuncs) evaluating
 the same C2 expression on the same full-size inputs for ~10 s on the host.
@@ -145,6 +146,60 @@ class Prepared:
         self.env.clear()
 
 
+class PreparedBatch:
+    """Structurally identical programs (attention heads) with device-resident
+    buffers and per-stage pointer tables, for timing batched launches."""
+
+    def __init__(self, programs):
+        from metellus_amd.api import compile_program
+        from metellus_amd.runtime import hip_backend
+        from metellus_amd.runtime.buffer import Buffer
+
+        self.hip = hip_backend
+        self.B = len(programs)
+        self.programs = programs
+        self.groups = compile_program(programs[0], batch=self.B)
+        per = [compile_program(p, batch=self.B) for p in programs[1:]]
+        for gs in per:
+            assert [g.kernel.source for g in gs] == [g.kernel.source for g in self.groups]
+        self.envs = []
+        for ops in programs:
+            env = {}
+            nbytes = {op.out.buffer_key: op.out.nbytes for op in ops.build()}
+            for name, arr in ops.uploads.items():
+                env[name] = Buffer.from_numpy(arr)
+            for g in self.groups:
+                for k in g.bindings:
+                    if k not in env:
+                        env[k] = Buffer(nbytes[k])
+            self.envs.append(env)
+        self.tables = []
+        for g in self.groups:
+            tabs = [
+                Buffer.from_numpy(np.array([env[k].device_address for env in self.envs], dtype=np.uint64))
+                for k in g.bindings
+            ]
+            self.tables.append(tabs)
+            _ = g.kernel.batched().handle
+        self.owner = {t.name: t for t in programs[0].tensors.values() if t.buffer_key == t.name}
+
+    def launch(self, i, timed=False):
+        g = self.groups[i]
+        k = g.kernel.batched()
+        return self.hip.launch(
+            k.handle, self.tables[i], g.dims, k.dims_slot_index,
+            (g.grid[0], g.grid[1], g.grid[2] * self.B), g.threads, timed=timed,
+        )
+
+    def release(self):
+        for env in self.envs:
+            for b in env.values():
+                b.release()
+        for tabs in self.tables:
+            for b in tabs:
+                b.release()
+
+
 class Flusher:
     """Evicts the 256 MiB Infinity Cache by *reading* a 512 MiB buffer (a
     row-sum kernel of this framework).  A write-based flush (memset) would
@@ -191,6 +246,7 @@ def time_kernels(prep: Prepared, steps: int, warmup: int, flusher, label: str) -
                 flusher.flush()
             ms.append(prep.launch(i, timed=True))
         bound, work = kernel_work(g, prep.owner)
+        work *= getattr(prep, "B", 1)
         mean = float(np.mean(ms))
         if bound == "hbm":
             achieved = work / (mean * 1e-3) / 1e9
@@ -299,7 +355,6 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-flush", action="store_true")
-    ap.add_argument("--c5-heads", type=int, default=4)
     ap.add_argument(
         "--calibrate-copy",
         action="store_true",
@@ -412,11 +467,11 @@ def main() -> int:
             todo.append(("C4 MLP literal", lambda: _c4(False)))
             todo.append(("C4 MLP diamond", lambda: _c4(True)))
         if only in (None, "c5"):
-            for h in range(args.c5_heads):
-                todo.append((f"C5 attention head {h}", lambda h=h: _c5(h)))
+            todo.append(("C5 attention, 32 heads batched", lambda: [_c5(h) for h in range(32)]))
         for label, make in todo:
             log(f"[bench] {label}: preparing")
-            prep = Prepared(make())
+            made = make()
+            prep = PreparedBatch(made) if isinstance(made, list) else Prepared(made)
             per_config += time_kernels(prep, extra_steps, 2, flush, label)
             prep.release()
     if line is None:

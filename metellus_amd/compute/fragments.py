@@ -27,6 +27,7 @@ from __future__ import annotations
 import functools
 import math
 import os
+import re
 import textwrap
 from dataclasses import dataclass
 from typing import Any, Literal
@@ -61,6 +62,7 @@ class CodegenContext:
     preamble: tuple[str, ...] = ()
     dims_buffer_index: int | None = None
     tg_z: int = 1
+    batched: bool = False
 
     @property
     def num_threads(self) -> int:
@@ -137,14 +139,36 @@ def device_header() -> str:
         return f.read()
 
 
+_PARAM_RE = re.compile(r"^\s*(const\s+)?float\s*\*\s*__restrict__\s+(\w+)\s*$")
+
+
+def batched_params(buffers: tuple[str, ...]) -> tuple[list[str], list[str]]:
+    """Batched variant of a kernel signature: every ``[const] float*
+    __restrict__ g_X`` parameter becomes a device table of per-program
+    pointers ``g_X_tab`` and the body starts by picking entry ``blockIdx.z``."""
+    params, picks = [], []
+    for decl in buffers:
+        m = _PARAM_RE.match(decl)
+        if m is None:
+            raise ValueError(f"cannot batch kernel parameter {decl!r}")
+        const, name = m.group(1) or "", m.group(2)
+        params.append(f"{const}float* const* __restrict__ {name}_tab")
+        picks.append(f"{const}float* __restrict__ {name} = {name}_tab[blockIdx.z];")
+    return params, picks
+
+
 class CodegenEngine:
     def render(self, fragments: list[KernelFragment], ctx: CodegenContext) -> str:
         dims_index = ctx.dims_buffer_index if ctx.dims_buffer_index is not None else len(ctx.buffers)
         if len(ctx.dims) > MAX_DIMS:
             raise ValueError(f"at most {MAX_DIMS} dims per kernel; got {len(ctx.dims)}")
-        params = list(ctx.buffers)
+        if ctx.batched:
+            params, picks = batched_params(ctx.buffers)
+        else:
+            params, picks = list(ctx.buffers), []
         params.insert(dims_index, "const mt_dims dims")
         body_parts = [
+            *picks,
             self._dim_decls(ctx.dims),
             *ctx.preamble,
             *ctx.threadgroup_decls,

@@ -119,9 +119,23 @@ DUAL_ANCHOR_TILES = (
 )
 
 
-def select_tile_config(M: int, K: int, N: int, anchors: int = 1) -> TileConfig:
-    cands = SINGLE_ANCHOR_TILES if anchors == 1 else DUAL_ANCHOR_TILES
+def _pow2_at_least(x: int) -> int:
+    p = 32
+    while p < x:
+        p *= 2
+    return p
+
+
+def select_tile_config(M: int, K: int, N: int, anchors: int = 1, batch: int = 1) -> TileConfig:
+    """``batch`` identical problems launched together (grid z) count toward
+    filling the GPU.  Tiles wider than the (power-of-two rounded) output are
+    skipped: their extra rows/columns would be masked-out work."""
+    cands = tuple(
+        t
+        for t in (SINGLE_ANCHOR_TILES if anchors == 1 else DUAL_ANCHOR_TILES)
+        if t.tile_M <= _pow2_at_least(M) and t.tile_N <= _pow2_at_least(N)
+    )
     for t in cands:
-        if ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N) >= NUM_CUS:
+        if batch * ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N) >= NUM_CUS:
             return t
     return max(cands, key=lambda t: (ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N), -t.tile_M * t.tile_N))

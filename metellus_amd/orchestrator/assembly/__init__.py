@@ -28,11 +28,14 @@ _ELEMENTWISE = {FusionStrategy.STANDALONE_ELEMENTWISE, FusionStrategy.ELEMENTWIS
 _MULTI = {FusionStrategy.MULTI_PRODUCER_CONVERGENT, FusionStrategy.DIAMOND_SHARED}
 
 
-def assemble(vertex: Vertex, *, function_name: str | None = None) -> KernelGroup:
+def assemble(vertex: Vertex, *, function_name: str | None = None, batch: int = 1) -> KernelGroup:
+    """``batch`` > 1: the kernel will be launched for that many identical
+    programs at once (``Kernel.batched``); matmul tiles are chosen for the
+    combined grid."""
     decision = classify(vertex)
     s = decision.strategy
     if s in _MATMUL:
-        return assemble_matmul(decision, function_name)
+        return assemble_matmul(decision, function_name, batch=batch)
     if s in _REDUCTION:
         return assemble_reduction(decision, function_name)
     if s in _ELEMENTWISE:
@@ -40,7 +43,7 @@ def assemble(vertex: Vertex, *, function_name: str | None = None) -> KernelGroup
     if s is FusionStrategy.STANDALONE_SHAPE:
         return assemble_shape(decision, function_name)
     if s in _MULTI:
-        return assemble_multi_anchor(decision, function_name)
+        return assemble_multi_anchor(decision, function_name, batch=batch)
     raise ValueError(f"unknown strategy {s!r}")
 
 

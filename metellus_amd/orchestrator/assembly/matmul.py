@@ -88,7 +88,7 @@ def operand_load(
     )
 
 
-def assemble_matmul(decision: DecisionView, function_name: str | None) -> KernelGroup:
+def assemble_matmul(decision: DecisionView, function_name: str | None, batch: int = 1) -> KernelGroup:
     anchor = decision.anchor
     assert isinstance(anchor, MatmulOp)
     src_a = decision.prologue_a[0].operands[0] if decision.prologue_a else anchor.a
@@ -96,7 +96,7 @@ def assemble_matmul(decision: DecisionView, function_name: str | None) -> Kernel
     assert isinstance(src_a, Tensor) and isinstance(src_b, Tensor)
     M, K = anchor.a.shape
     N = anchor.b.shape[1]
-    tile = select_tile_config(M, K, N)
+    tile = select_tile_config(M, K, N, batch=batch)
     aligned = is_aligned_shape(M, K, N, tile)
     final_out = decision.epilogue[-1].out if decision.epilogue else anchor.out
     out_key = final_out.buffer_key

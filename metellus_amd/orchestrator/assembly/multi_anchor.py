@@ -35,7 +35,7 @@ from metellus_amd.orchestrator.kernel_group import KernelGroup
 from metellus_amd.runtime.program import Kernel
 
 
-def assemble_multi_anchor(decision: DecisionView, function_name: str | None) -> KernelGroup:
+def assemble_multi_anchor(decision: DecisionView, function_name: str | None, batch: int = 1) -> KernelGroup:
     anchors = decision.anchors
     merge = decision.merge_elem
     assert anchors is not None and len(anchors) == 2 and merge is not None
@@ -50,7 +50,7 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None) -> 
     src_b = tuple(pro_b[i][0].operands[0] if pro_b[i] else anchors[i].b for i in range(2))
     assert all(isinstance(t, Tensor) for t in (*src_a, *src_b))
     out_key = merge.out.buffer_key
-    tile = select_tile_config(M, max(K0, K1), N, anchors=2)
+    tile = select_tile_config(M, max(K0, K1), N, anchors=2, batch=batch)
     aligned = is_aligned_shape(M, K0, N, tile) and is_aligned_shape(M, K1, N, tile)
 
     order = (src_a[0], src_b[0], src_b[1]) if shared else (src_a[0], src_b[0], src_a[1], src_b[1])

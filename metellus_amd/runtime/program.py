@@ -146,6 +146,21 @@ class Kernel:
     def execute(self, env: Env) -> None:
         _ = self.source
 
+    def batched(self) -> "Kernel":
+        """The same kernel for a batch of identical programs: buffer
+        parameters become per-program pointer tables indexed by blockIdx.z
+        (launch with grid z = batch size)."""
+        if self.ctx.batched:
+            return self
+        cached = getattr(self, "_batched", None)
+        if cached is None:
+            import dataclasses
+
+            ctx = dataclasses.replace(self.ctx, batched=True, function_name=self.ctx.function_name + "_batched")
+            cached = Kernel(self.fragments, ctx, self.compile_options)
+            self._batched = cached
+        return cached
+
 
 @dataclass(frozen=True)
 class Dispatch:

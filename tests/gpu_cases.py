@@ -90,12 +90,22 @@ def mlp_block(M: int, D: int, H: int, seed: int = 3, diamond: bool = False) -> O
     return ops
 
 
+_QKV_CACHE: dict = {}
+
+
+def attention_qkv(S: int, Dh: int, seed: int = 4, heads: int = 1):
+    """Q, K, V of shape (heads, S, Dh), N(0, 1), drawn in that order."""
+    key = (S, Dh, seed, heads)
+    if key not in _QKV_CACHE:
+        rng = np.random.default_rng(seed)
+        _QKV_CACHE.clear()
+        _QKV_CACHE[key] = tuple(rng.standard_normal((heads, S, Dh)).astype(np.float32) for _ in range(3))
+    return _QKV_CACHE[key]
+
+
 def attention_head(S: int, Dh: int, seed: int = 4, head: int = 0, heads: int = 1) -> Operations:
     """C5 (one head): softmax((Q @ K^T) / sqrt(Dh)) @ V, K^T a stride view."""
-    rng = np.random.default_rng(seed)
-    q = rng.standard_normal((heads, S, Dh)).astype(np.float32)
-    k = rng.standard_normal((heads, S, Dh)).astype(np.float32)
-    v = rng.standard_normal((heads, S, Dh)).astype(np.float32)
+    q, k, v = attention_qkv(S, Dh, seed, heads)
     ops = Operations()
     ops.from_numpy(np.ascontiguousarray(q[head]), "Q")
     ops.from_numpy(np.ascontiguousarray(k[head]), "K")
