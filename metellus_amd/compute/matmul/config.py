@@ -96,11 +96,15 @@ def grid_for(M: int, N: int, config: TileConfig) -> tuple[int, int, int]:
     return (ceil_div(N, config.tile_N), ceil_div(M, config.tile_M), 1)
 
 
-# Largest first.  One accumulator set: wave tiles up to 128x64 (128 acc regs).
+# Candidate tiles.  One accumulator set: wave tiles up to 128x64 (128 acc
+# registers); two sets (multi-anchor): up to 64x64 per anchor.
 SINGLE_ANCHOR_TILES = (
     TileConfig(256, 256, 32, 2, 4),
+    TileConfig(256, 128, 32, 4, 2),
+    TileConfig(128, 256, 32, 2, 4),
     TileConfig(256, 128, 32, 2, 2),
     TileConfig(128, 256, 32, 2, 2),
+    TileConfig(128, 128, 32, 4, 2),
     TileConfig(128, 128, 32, 2, 2),
     TileConfig(128, 64, 32, 2, 2),
     TileConfig(64, 128, 32, 2, 2),
@@ -108,7 +112,6 @@ SINGLE_ANCHOR_TILES = (
     TileConfig(32, 32, 32, 1, 1),
 )
 
-# Two accumulator sets (multi-anchor): wave tiles up to 64x64 per anchor.
 DUAL_ANCHOR_TILES = (
     TileConfig(256, 128, 32, 4, 2),
     TileConfig(128, 128, 32, 2, 2),
@@ -118,6 +121,11 @@ DUAL_ANCHOR_TILES = (
     TileConfig(32, 32, 32, 1, 1),
 )
 
+LDS_BYTES = 163_840
+VGPRS_PER_LANE = 512  # unified VGPR+AGPR file per SIMD lane (gfx950)
+
+FORCE_TILE: TileConfig | None = None  # tuning override (measurement scripts)
+
 
 def _pow2_at_least(x: int) -> int:
     p = 32
@@ -126,16 +134,54 @@ def _pow2_at_least(x: int) -> int:
     return p
 
 
+def tile_lds_bytes(t: TileConfig, anchors: int = 1) -> int:
+    return 4 * t.stages * (t.tile_M * t.lda + anchors * t.tile_K * t.ldb)
+
+
+def estimated_vgprs(t: TileConfig, anchors: int = 1) -> int:
+    """Accumulators + prefetch registers + ~48 for addressing/operands."""
+    acc = 16 * t.WM * t.WN * anchors
+    prefetch = (t.tile_M * t.tile_K + anchors * t.tile_K * t.tile_N) // t.num_threads
+    return acc + prefetch + 48
+
+
+def tile_score(t: TileConfig, M: int, N: int, anchors: int = 1, batch: int = 1) -> tuple[float, float]:
+    """(score, waves per SIMD).  Score = tile area (operand reuse per byte
+    loaded) x resident waves per SIMD (latency hiding, capped at 4; from the
+    LDS and register limits and the number of workgroups available) x the
+    fraction of the tile that is real output x how well the grid fills the
+    256 CUs."""
+    wgs = batch * ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N)
+    waves = t.sg_M * t.sg_N
+    by_lds = LDS_BYTES // tile_lds_bytes(t, anchors)
+    by_vgpr = max(1, (4 * (VGPRS_PER_LANE // estimated_vgprs(t, anchors))) // waves)
+    per_cu = max(1, min(by_lds, by_vgpr, ceil_div(wgs, NUM_CUS)))
+    wps = per_cu * waves / 4
+    useful = (M * N) / (ceil_div(M, t.tile_M) * t.tile_M * ceil_div(N, t.tile_N) * t.tile_N)
+    fill = min(1.0, wgs / NUM_CUS)
+    return t.tile_M * t.tile_N * min(wps, 4.0) * useful * fill, wps
+
+
 def select_tile_config(M: int, K: int, N: int, anchors: int = 1, batch: int = 1) -> TileConfig:
-    """``batch`` identical problems launched together (grid z) count toward
-    filling the GPU.  Tiles wider than the (power-of-two rounded) output are
-    skipped: their extra rows/columns would be masked-out work."""
-    cands = tuple(
+    """Highest ``tile_score``; ties go to more resident waves, then more
+    workgroups.  ``batch``
+    identical problems launched together (grid z) count toward filling the
+    GPU.  Tiles wider than the (power-of-two rounded) output are skipped.
+    Measured on MI355X: 256x256 (8 waves) for 4096^3 and the C4/C5 Q.K^T
+    GEMMs; 128x128 (8 waves) for the C5 P.V GEMM (N = 128, batched heads)."""
+    if FORCE_TILE is not None:
+        return FORCE_TILE
+    cands = [
         t
         for t in (SINGLE_ANCHOR_TILES if anchors == 1 else DUAL_ANCHOR_TILES)
         if t.tile_M <= _pow2_at_least(M) and t.tile_N <= _pow2_at_least(N)
-    )
-    for t in cands:
-        if batch * ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N) >= NUM_CUS:
-            return t
-    return max(cands, key=lambda t: (ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N), -t.tile_M * t.tile_N))
+    ]
+    best = None
+    best_key = None
+    for i, t in enumerate(cands):
+        score, wps = tile_score(t, M, N, anchors, batch)
+        wgs = ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N)
+        key = (score, wps, wgs, -i)
+        if best_key is None or key > best_key:
+            best, best_key = t, key
+    return best

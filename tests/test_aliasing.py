@@ -87,7 +87,7 @@ def test_multi_producer_lifetimes_and_rewrite():
     late = [a for a in aliases if a.new_name in ("A1_tile", "B1_tile")]
     assert any(not a.preceded_by_barrier for a in late)
     src = aliased.kernel.source
-    assert "float (*A1_tile)[32][36] = reinterpret_cast<float (*)[32][36]>(_A0_tile_storage);" in src
+    assert "float (*A1_tile)[64][36] = reinterpret_cast<float (*)[64][36]>(_A0_tile_storage);" in src
 
 
 def test_single_tenant_kernels_are_unchanged():

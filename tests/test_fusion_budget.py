@@ -1,11 +1,11 @@
 """The LDS budget gate of ``fuse`` (the reference's
 tests/test_fusion_budget.py, re-derived for gfx950 tiles).
 
-gfx950 numbers used below (32x32x32 MFMA tile for 64x64 operands, LDS rows
-padded to 36 floats, double-buffered): one matmul = A 2x32x36 + B 2x32x36
-floats = 18,432 B; the diamond (shared A, two B chunks) = 27,648 B; the
-non-shared multi-producer = 18,432 B because its second mainloop's tiles
-alias the first's.  The real cap is 163,840 B."""
+gfx950 numbers used below (64x64x32 MFMA tile for 64x64 operands, A rows
+padded to 36 floats and B rows to 68, double-buffered): one matmul = A
+2x64x36 + B 2x32x68 floats = 35,840 B; the diamond (shared A, two B chunks)
+= 53,248 B; the non-shared multi-producer = 35,840 B because its second
+mainloop's tiles alias the first's.  The real cap is 163,840 B."""
 
 import pytest
 
@@ -56,28 +56,28 @@ def test_fits_under_cap_unchanged():
 def test_budget_numbers():
     (d,) = fuse(_pair(True).build())
     (m,) = fuse(_pair(False).build())
-    assert _budget(d) == 27_648
-    assert _budget(m) == 18_432  # A1/B1 alias A0/B0
+    assert _budget(d) == 53_248
+    assert _budget(m) == 35_840  # A1/B1 alias A0/B0
     ops = Operations()
     ops.input("A", shape=(64, 64))
     ops.input("B", shape=(64, 64))
     ops.matmul(a="A", b="B", out="C")
     (p,) = fuse(ops.build())
-    assert _budget(p) == 18_432
+    assert _budget(p) == 35_840
 
 
 def test_overflowing_fusion_is_blacklisted_and_split(monkeypatch):
-    monkeypatch.setattr("orchestrator.fusion.TGMEM_CAP_BYTES", 24_576)
+    monkeypatch.setattr("orchestrator.fusion.TGMEM_CAP_BYTES", 45_056)
     vs = fuse(_pair(True).build())
     assert len(vs) > 1
     for v in vs:
-        assert _budget(v) <= 24_576
+        assert _budget(v) <= 45_056
     groups = sorted(tuple(sorted(type(op).__name__ for op in v.ops)) for v in vs)
     assert ("MatmulOp",) in groups
 
 
 def test_aliasing_lets_multi_producer_fit_where_diamond_cannot(monkeypatch):
-    monkeypatch.setattr("orchestrator.fusion.TGMEM_CAP_BYTES", 24_576)
+    monkeypatch.setattr("orchestrator.fusion.TGMEM_CAP_BYTES", 45_056)
     (v,) = fuse(_pair(False).build())
     assert assemble(v).strategy is FusionStrategy.MULTI_PRODUCER_CONVERGENT
 
@@ -94,7 +94,7 @@ def test_irreducible_primitive_raises(monkeypatch):
 
 
 def test_blacklist_retry_is_deterministic(monkeypatch):
-    monkeypatch.setattr("orchestrator.fusion.TGMEM_CAP_BYTES", 24_576)
+    monkeypatch.setattr("orchestrator.fusion.TGMEM_CAP_BYTES", 45_056)
     a = fuse(_pair(True).build())
     b = fuse(_pair(True).build())
     assert [[type(op).__name__ for op in v.ops] for v in a] == [[type(op).__name__ for op in v.ops] for v in b]
