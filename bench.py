@@ -204,12 +204,16 @@ class Flusher:
     """Evicts the 256 MiB Infinity Cache by *reading* a 512 MiB buffer (a
     row-sum kernel of this framework).  A write-based flush (memset) would
     leave dirty lines whose write-back then lands inside the measured
-    kernel; after a read flush the cache holds only clean lines."""
+    kernel; after a read flush the cache holds only clean lines.  The flush
+    kernel is built with ordinary (allocating) loads: nontemporal loads,
+    the product default for row reductions, would leave the cache contents
+    -- dirty output lines included -- in place."""
 
     ROWS, COLS = 16384, 8192  # 512 MiB of fp32
 
     def __init__(self):
         from metellus_amd.api import compile_program
+        from metellus_amd.compute.reduction import reduction as red
         from metellus_amd.orchestrator import Operations
         from metellus_amd.runtime import hip_backend
         from metellus_amd.runtime.buffer import Buffer
@@ -217,7 +221,12 @@ class Flusher:
         ops = Operations()
         ops.input("flush_src", (self.ROWS, self.COLS))
         ops.reduction("sum", out="flush_sum", x="flush_src")
-        (self.group,) = compile_program(ops)
+        saved, red.NT_LOAD = red.NT_LOAD, False
+        try:
+            (self.group,) = compile_program(ops)
+        finally:
+            red.NT_LOAD = saved
+        assert "mt_ld4_nt" not in self.group.kernel.source.split('extern "C"')[1]
         self.src = Buffer(self.ROWS * self.COLS * 4)
         self.src.fill(0)
         self.dst = Buffer(self.ROWS * 4)

@@ -141,6 +141,13 @@ class ChainCode:
                     extras.add_tensor(op.operands[pos], base_slot)
 
     @property
+    def broadcast_operands_only(self) -> bool:
+        """True when every external operand is a row, column or scalar
+        broadcast (small, cache-resident reads)."""
+        small = (BroadcastSpec.ROW, BroadcastSpec.COL, BroadcastSpec.SCALAR)
+        return all(e.broadcast in small for e in self.externals)
+
+    @property
     def arity(self) -> int:
         return len(self.seeds) + len(self.externals)
 

@@ -145,15 +145,21 @@ _PARAM_RE = re.compile(r"^\s*(const\s+)?float\s*\*\s*__restrict__\s+(\w+)\s*$")
 def batched_params(buffers: tuple[str, ...]) -> tuple[list[str], list[str]]:
     """Batched variant of a kernel signature: every ``[const] float*
     __restrict__ g_X`` parameter becomes a device table of per-program
-    pointers ``g_X_tab`` and the body starts by picking entry ``blockIdx.z``."""
+    pointers ``g_X_tab`` and the body starts by picking entry ``blockIdx.z``.
+
+    The table entries are typed as global-address-space pointers: a pointer
+    read from memory is otherwise generic, every access through it becomes a
+    flat instruction, and flat loads also count against the LDS wait counter,
+    so each LDS read of a pipelined mainloop would wait for the next chunk's
+    global loads."""
     params, picks = [], []
     for decl in buffers:
         m = _PARAM_RE.match(decl)
         if m is None:
             raise ValueError(f"cannot batch kernel parameter {decl!r}")
         const, name = m.group(1) or "", m.group(2)
-        params.append(f"{const}float* const* __restrict__ {name}_tab")
-        picks.append(f"{const}float* __restrict__ {name} = {name}_tab[blockIdx.z];")
+        params.append(f"{const}MT_GLOBAL float* const* __restrict__ {name}_tab")
+        picks.append(f"{const}float* __restrict__ {name} = ({const}float*){name}_tab[blockIdx.z];")
     return params, picks
 
 

@@ -162,6 +162,30 @@ def tile_score(t: TileConfig, M: int, N: int, anchors: int = 1, batch: int = 1) 
     return t.tile_M * t.tile_N * min(wps, 4.0) * useful * fill, wps
 
 
+PERSISTENT = True  # tuning switch for the persistent tile loop
+PERSISTENT_CAPACITY: int | None = None  # override of resident workgroups (tests)
+
+
+def resident_workgroups(t: TileConfig, anchors: int = 1) -> int:
+    """Workgroups of tile ``t`` one compute unit holds at once, from the LDS
+    size and the register estimate (4 SIMDs x 512 registers per lane)."""
+    by_lds = LDS_BYTES // tile_lds_bytes(t, anchors)
+    by_vgpr = (4 * (VGPRS_PER_LANE // estimated_vgprs(t, anchors))) // (t.sg_M * t.sg_N)
+    return max(1, min(by_lds, by_vgpr))
+
+
+def persistent_workgroups(M: int, N: int, t: TileConfig, batch: int = 1) -> int | None:
+    """Workgroups per problem for a persistent tile loop, or None when every
+    tile of every problem gets a resident workgroup in one round anyway."""
+    if not PERSISTENT or t.stages != 2:
+        return None
+    tiles = ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N)
+    capacity = PERSISTENT_CAPACITY or NUM_CUS * resident_workgroups(t)
+    if tiles * batch <= capacity:
+        return None
+    return min(tiles, max(1, capacity // batch))
+
+
 def select_tile_config(M: int, K: int, N: int, anchors: int = 1, batch: int = 1) -> TileConfig:
     """Highest ``tile_score``; ties go to more resident waves, then more
     workgroups.  ``batch``

@@ -46,14 +46,65 @@ class MatmulConfig:
 
 
 @dataclass(frozen=True)
-class MatmulTileMappingFragment:
-    """``tg`` = (column tile, row tile) of this workgroup."""
+class PersistentTiles:
+    """Persistent tile loop: a grid of (P, 1, batch) workgroups, workgroup x
+    taking output tiles x, x + P, x + 2P, ... (row-major over the
+    ``ceil(M / tile_M) x ceil(N / tile_N)`` tiles).  Used when the tiles
+    outnumber the workgroups the GPU holds at once: the next tile's first
+    k-chunk is then loaded during the current tile's last one, and the
+    current tile's stores drain while the next tile's MFMAs run, instead of
+    each workgroup paying its own launch, first load and store phases."""
 
+    tile_M: int
+    tile_N: int
+    M_dim_var: str = "M"
+    N_dim_var: str = "N"
+
+
+@dataclass(frozen=True)
+class MatmulTileMappingFragment:
+    """``tg`` = (column tile, row tile) of this workgroup; with ``persistent``
+    it opens the tile loop (closed by ``PersistentLoopEndFragment``) and
+    defines ``mt_first_tile``, ``mt_has_next``, ``mt_next_m0/n0`` for the
+    mainloop's cross-tile prefetch."""
+
+    persistent: PersistentTiles | None = None
     name: str = "tile_mapping"
     kind: str = "setup"
 
     def render(self, ctx: CodegenContext) -> str:
-        return "const uint3 tg = make_uint3(blockIdx.x, blockIdx.y, blockIdx.z);"
+        p = self.persistent
+        if p is None:
+            return "const uint3 tg = make_uint3(blockIdx.x, blockIdx.y, blockIdx.z);"
+        return "\n".join(
+            [
+                f"const unsigned mt_tiles_x = ({p.N_dim_var} + {p.tile_N - 1}u) / {p.tile_N}u;",
+                f"const unsigned mt_tiles = mt_tiles_x * (({p.M_dim_var} + {p.tile_M - 1}u) / {p.tile_M}u);",
+                "unsigned mt_stage = 0u;  // LDS buffer holding the current k-chunk",
+                "for (unsigned mt_t = blockIdx.x; mt_t < mt_tiles; mt_t += gridDim.x) {",
+                "const bool mt_first_tile = mt_t == blockIdx.x;",
+                "const unsigned mt_t_next = mt_t + gridDim.x;",
+                "const bool mt_has_next = mt_t_next < mt_tiles;",
+                f"const unsigned mt_next_m0 = (mt_t_next / mt_tiles_x) * {p.tile_M}u;",
+                f"const unsigned mt_next_n0 = (mt_t_next % mt_tiles_x) * {p.tile_N}u;",
+                "const uint3 tg = make_uint3(mt_t % mt_tiles_x, mt_t / mt_tiles_x, blockIdx.z);",
+            ]
+        )
+
+    @property
+    def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
+        return ()
+
+
+@dataclass(frozen=True)
+class PersistentLoopEndFragment:
+    """Closes the persistent tile loop opened by the tile mapping."""
+
+    name: str = "persistent_loop_end"
+    kind: str = "setup"
+
+    def render(self, ctx: CodegenContext) -> str:
+        return "}  // persistent tile loop"
 
     @property
     def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
@@ -163,11 +214,18 @@ class MatmulMainloopFragment:
 
     With two LDS buffers one barrier per chunk suffices: buffer b is written
     in iteration kt only after every lane passed the barrier that ended
-    iteration kt-1, the last reader of b."""
+    iteration kt-1, the last reader of b.
+
+    ``persistent`` (inside a persistent tile loop): the buffer index is the
+    running ``mt_stage``, flipped after every chunk of every tile; only the
+    first tile loads chunk 0 before its loop, and the last iteration of each
+    tile loads chunk 0 of the next tile (``mt_next_m0/n0``) into the other
+    buffer, so the same one-barrier-per-chunk argument spans tiles."""
 
     tile_K: int
     fragments: tuple[KernelFragment, ...]
     K_dim_var: str
+    persistent: bool = False
     name: str = "matmul_mainloop"
     kind: str = "compute"
 
@@ -194,6 +252,10 @@ class MatmulMainloopFragment:
                 "}",
             ]
             return "{\n" + textwrap.indent("\n".join(body), "    ") + "\n}"
+        if self.persistent:
+            if stages != 2:
+                raise ValueError("a persistent tile loop needs double-buffered LDS tiles")
+            return self._render_persistent(loads, computes, body)
         body += [
             f"const unsigned n_chunks = ({kvar} + {tk - 1}u) / {tk}u;",
             "{",
@@ -214,6 +276,38 @@ class MatmulMainloopFragment:
             *[f"        {ld.render_commit('cur ^ 1u')}" for ld in loads],
             "    }",
             "    __syncthreads();",
+            "}",
+        ]
+        return "{\n" + textwrap.indent("\n".join(body), "    ") + "\n}"
+
+    def _render_persistent(self, loads, computes, body: list[str]) -> str:
+        kvar, tk = self.K_dim_var, self.tile_K
+        body += [
+            f"const unsigned n_chunks = ({kvar} + {tk - 1}u) / {tk}u;",
+            "if (mt_first_tile) {",
+            "    const unsigned k_chunk = 0u;",
+            *[f"    {ld.render_fetch()}" for ld in loads],
+            *[f"    {ld.render_commit('mt_stage')}" for ld in loads],
+            "    __syncthreads();",
+            "}",
+            "for (unsigned kt = 0; kt < n_chunks; ++kt) {",
+            "    const unsigned cur = mt_stage;",
+            "    const bool more = kt + 1u < n_chunks;",
+            "    if (more) {",
+            f"        const unsigned k_chunk = (kt + 1u) * {tk}u;",
+            *[f"        {ld.render_fetch()}" for ld in loads],
+            "    } else if (mt_has_next) {",
+            "        const unsigned tile_m0 = mt_next_m0;",
+            "        const unsigned tile_n0 = mt_next_n0;",
+            "        const unsigned k_chunk = 0u;",
+            *[f"        {ld.render_fetch()}" for ld in loads],
+            "    }",
+            *[f"    {c.render_stage('cur')}" for c in computes],
+            "    if (more || mt_has_next) {",
+            *[f"        {ld.render_commit('cur ^ 1u')}" for ld in loads],
+            "    }",
+            "    __syncthreads();",
+            "    mt_stage ^= 1u;",
             "}",
         ]
         return "{\n" + textwrap.indent("\n".join(body), "    ") + "\n}"
@@ -333,5 +427,7 @@ __all__ = [
     "MatmulRegisterEpilogueFragment",
     "MatmulSetupFragment",
     "MatmulTileMappingFragment",
+    "PersistentLoopEndFragment",
+    "PersistentTiles",
     "ThreadIndexFragment",
 ]

@@ -34,10 +34,13 @@ REDUCTION_OPS = ("sum", "max", "min", "product")
 
 ValueTransform = Callable[[str], str]
 
-# Measured on MI355X (8192^2 rows, cache flushed): 16 float4 in flight per
-# lane with ordinary loads reads at ~6.9 TB/s.
+# Measured on MI355X with the caches flushed by a read pass before each
+# launch: nontemporal loads take an 8192^2 row reduction from ~48 us to
+# ~42.5 us (6.3 TB/s) and the 32-head 2048^2 attention reductions from
+# ~89 us to ~81 us (6.6 TB/s); unroll 4..32 and 1..4 waves per row move
+# either by less than run-to-run noise.
 UNROLL = 16  # float4 chunks (or elements) in flight per lane
-NT_LOAD = False  # nontemporal (streaming) row loads
+NT_LOAD = True  # nontemporal (streaming) row loads
 
 
 def _identity(op: str) -> str:

@@ -10,7 +10,13 @@
 //   * mt_tile_colvec / rowvec / scalar
 //                             cooperative ROWS x COLS tile fetch: global ->
 //                             registers (transform applied to in-bounds
-//                             elements, 0 outside), then registers -> LDS
+//                             elements, 0 outside), then registers -> LDS;
+//                             fetch_raw + commit_xf apply the transform at
+//                             commit time instead, so the global loads stay
+//                             in flight across the MFMAs of the current chunk
+//   * MT_GLOBAL               global address space qualifier (pointer tables
+//                             of batched kernels hold global pointers, which
+//                             keeps their loads global_load, not flat_load)
 //   * mt_mfma_tile            fp32 MFMA (v_mfma_f32_32x32x2f32) over one LDS
 //                             k-chunk for a wave's WM x WN grid of 32x32 blocks
 //   * mt_acc_row              row of accumulator register v in a 32x32 block
@@ -25,6 +31,7 @@ struct mt_dims {
 };
 
 #define MT_INLINE __device__ __forceinline__
+#define MT_GLOBAL __attribute__((address_space(1)))
 
 #ifndef INFINITY
 #define INFINITY __builtin_inff()
@@ -130,6 +137,35 @@ struct mt_tile_colvec {
             }
         }
     }
+
+    // Deferred transform: fetch_raw keeps the loaded values untouched (0
+    // outside the bounds) and remembers the tile origin; commit_xf applies f
+    // to the in-bounds elements on the way to LDS.
+    unsigned r0, c0, rl, cl;
+
+    template <bool CHECK>
+    MT_INLINE void fetch_raw(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
+                             unsigned rlim, unsigned clim, unsigned tid) {
+        r0 = row0, c0 = col0, rl = rlim, cl = clim;
+        fetch<CHECK>(src, rs, row0, col0, rlim, clim, tid, mt_identity{});
+    }
+
+    template <int LD, bool CHECK, typename F>
+    MT_INLINE void commit_xf(float* lds, unsigned tid, F f) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / CV, c = (idx % CV) * 4u;
+            const unsigned gr = r0 + r, gc = c0 + c;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rl && gc < cl))) {
+                v[i].x = f(v[i].x, gr, gc);
+                v[i].y = f(v[i].y, gr, gc + 1u);
+                v[i].z = f(v[i].z, gr, gc + 2u);
+                v[i].w = f(v[i].w, gr, gc + 3u);
+            }
+        }
+        commit<LD>(lds, tid);
+    }
 };
 
 // Vectorised along rows: rs == 1, cs % 4 == 0, ROWS % 4 == 0, rlim % 4 == 0.
@@ -174,6 +210,32 @@ struct mt_tile_rowvec {
             }
         }
     }
+
+    unsigned r0, c0, rl, cl;
+
+    template <bool CHECK>
+    MT_INLINE void fetch_raw(const float* __restrict__ src, unsigned cs, unsigned row0, unsigned col0,
+                             unsigned rlim, unsigned clim, unsigned tid) {
+        r0 = row0, c0 = col0, rl = rlim, cl = clim;
+        fetch<CHECK>(src, cs, row0, col0, rlim, clim, tid, mt_identity{});
+    }
+
+    template <int LD, bool CHECK, typename F>
+    MT_INLINE void commit_xf(float* lds, unsigned tid, F f) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned c = idx / RV, r = (idx % RV) * 4u;
+            const unsigned gr = r0 + r, gc = c0 + c;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rl && gc < cl))) {
+                v[i].x = f(v[i].x, gr, gc);
+                v[i].y = f(v[i].y, gr + 1u, gc);
+                v[i].z = f(v[i].z, gr + 2u, gc);
+                v[i].w = f(v[i].w, gr + 3u, gc);
+            }
+        }
+        commit<LD>(lds, tid);
+    }
 };
 
 // Any strides: one element per load.
@@ -209,6 +271,29 @@ struct mt_tile_scalar {
                 lds[r * LD + c] = v[i];
             }
         }
+    }
+
+    unsigned r0, c0, rl, cl;
+
+    template <bool CHECK>
+    MT_INLINE void fetch_raw(const float* __restrict__ src, unsigned rs, unsigned cs, unsigned row0,
+                             unsigned col0, unsigned rlim, unsigned clim, unsigned tid) {
+        r0 = row0, c0 = col0, rl = rlim, cl = clim;
+        fetch<CHECK>(src, rs, cs, row0, col0, rlim, clim, tid, mt_identity{});
+    }
+
+    template <int LD, bool CHECK, typename F>
+    MT_INLINE void commit_xf(float* lds, unsigned tid, F f) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / COLS, c = idx % COLS;
+            const unsigned gr = r0 + r, gc = c0 + c;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rl && gc < cl))) {
+                v[i] = f(v[i], gr, gc);
+            }
+        }
+        commit<LD>(lds, tid);
     }
 };
 

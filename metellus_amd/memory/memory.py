@@ -61,6 +61,11 @@ class TgLoadFragment:
     stages: int = 1
     mode: str | None = None  # "colvec" | "rowvec" | "scalar" (default: from strides)
     transform_lambda: str | None = None
+    # Apply the transform when the registers are written to LDS rather than
+    # when the loads return, so a pipelined mainloop does not wait for the
+    # next chunk's loads before its MFMAs.  Worth it when the transform reads
+    # only small broadcast operands (those loads then happen at commit).
+    defer_transform: bool = False
 
     @property
     def pitch(self) -> int:
@@ -107,14 +112,20 @@ class TgLoadFragment:
         clim = self.col_limit if self.col_limit is not None else "0xffffffffu"
         check = "true" if self.check else "false"
         mode = self.resolved_mode()
-        head = f"{self.loader}.template fetch<{check}>({self.src_name}, "
+        deferred = self.defer_transform and self._has_transform()
+        verb = "fetch_raw" if deferred else "fetch"
+        head = f"{self.loader}.template {verb}<{check}>({self.src_name}, "
         if mode == "colvec":
             strides = f"{self.src_row_stride}"
         elif mode == "rowvec":
             strides = f"{self.src_col_stride}"
         else:
             strides = f"{self.src_row_stride}, {self.src_col_stride}"
-        return f"{head}{strides}, {self.row_start}, {self.col_start}, {rlim}, {clim}, threadIdx.x, {self.xform});"
+        tail = ")" if deferred else f", {self.xform})"
+        return f"{head}{strides}, {self.row_start}, {self.col_start}, {rlim}, {clim}, threadIdx.x{tail};"
+
+    def _has_transform(self) -> bool:
+        return self.transform_lambda is not None or self.value_transform is not None
 
     def stage_ptr(self, stage: str) -> str:
         if self.stages > 1:
@@ -122,6 +133,12 @@ class TgLoadFragment:
         return f"&{self.dst_name}[0][0]"
 
     def render_commit(self, stage: str = "0") -> str:
+        if self.defer_transform and self._has_transform():
+            check = "true" if self.check else "false"
+            return (
+                f"{self.loader}.template commit_xf<{self.pitch}, {check}>"
+                f"({self.stage_ptr(stage)}, threadIdx.x, {self.xform});"
+            )
         return f"{self.loader}.template commit<{self.pitch}>({self.stage_ptr(stage)}, threadIdx.x);"
 
     def render(self, ctx: CodegenContext) -> str:

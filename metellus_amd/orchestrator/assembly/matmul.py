@@ -10,13 +10,21 @@ transposed; K^T is read along K with 128-bit loads, no transpose kernel).
 gfx950 kernel: fp32 MFMA mainloop over double-buffered LDS, every epilogue
 applied to the accumulator registers (both ``MATMUL_EPILOGUE_REGISTER`` and
 ``MATMUL_EPILOGUE_TG``; the label records the reference's decision), then a
-direct store.  LDS holds only the A and B chunks.
+direct store.  LDS holds only the A and B chunks.  When the output tiles
+outnumber the workgroups resident at once, the grid is instead
+``(P, 1, 1)`` workgroups looping over tiles (``PersistentTiles``).
 """
 
 from __future__ import annotations
 
 from metellus_amd.compute.fragments import BarrierFragment, CodegenContext, lds_decl
-from metellus_amd.compute.matmul.config import TileConfig, grid_for, is_aligned_shape, select_tile_config
+from metellus_amd.compute.matmul.config import (
+    TileConfig,
+    grid_for,
+    is_aligned_shape,
+    persistent_workgroups,
+    select_tile_config,
+)
 from metellus_amd.compute.matmul.matmul import (
     MatmulComputeFragment,
     MatmulConfig,
@@ -24,6 +32,8 @@ from metellus_amd.compute.matmul.matmul import (
     MatmulMainloopFragment,
     MatmulSetupFragment,
     MatmulTileMappingFragment,
+    PersistentLoopEndFragment,
+    PersistentTiles,
     ThreadIndexFragment,
 )
 from metellus_amd.memory.memory import TgLoadFragment
@@ -85,6 +95,7 @@ def operand_load(
         stages=tile.stages,
         mode=mode,
         transform_lambda=lam,
+        defer_transform=prologue is not None and prologue.broadcast_operands_only,
     )
 
 
@@ -142,14 +153,24 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
                           M=M, K=K, N=N, aligned=aligned, prologue=pro_a)
     b_load = operand_load(name="load_B_tile", src=src_b, dst="B_tile", tile=tile, side="b",
                           M=M, K=K, N=N, aligned=aligned, prologue=pro_b)
+    n_persistent = persistent_workgroups(M, N, tile, batch)
+    persistent = PersistentTiles(tile.tile_M, tile.tile_N) if n_persistent else None
     mainloop = MatmulMainloopFragment(
         tile_K=tile.tile_K,
         fragments=(a_load, b_load, BarrierFragment("inputs_ready"), MatmulComputeFragment(config),
                    BarrierFragment("compute_done")),
         K_dim_var="K",
+        persistent=persistent is not None,
     )
     store = MatmulEpilogueStoreFragment(config, value_expr=value_expr, check=not aligned)
-    fragments = (MatmulTileMappingFragment(), ThreadIndexFragment(tile), MatmulSetupFragment(config), mainloop, store)
+    fragments = (
+        MatmulTileMappingFragment(persistent),
+        ThreadIndexFragment(tile),
+        MatmulSetupFragment(config),
+        mainloop,
+        store,
+        *((PersistentLoopEndFragment(),) if persistent else ()),
+    )
     ctx = CodegenContext(
         function_name=function_name or f"matmul_{anchor.out.name}_fused",
         buffers=(*(input_param(k) for k in slots), output_param(out_key), *extras.buffers),
@@ -163,7 +184,7 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         kernel=Kernel(fragments=fragments, ctx=ctx),
         bindings=(*slots, out_key, *extras.bindings),
         dims=(M, K, N),
-        grid=grid_for(M, N, tile),
+        grid=(n_persistent, 1, 1) if n_persistent else grid_for(M, N, tile),
         threads=(tile.tg_x, 1, 1),
         ops=decision.ops,
         strategy=decision.strategy,

@@ -1,0 +1,73 @@
+"""Code-generation choices that the GPU timings depend on, checked on the
+generated source (no GPU): where matmul prologues are applied, and how
+batched kernels address their per-program buffers."""
+
+from metellus_amd.api import compile_program
+from metellus_amd.runtime import hip_backend
+from tests import gpu_cases
+
+
+def _by_name(groups):
+    return {g.kernel.function_name: g for g in groups}
+
+
+def test_broadcast_only_prologue_is_applied_at_commit():
+    # P = e / s1 (a per-row divisor) folded into the P @ V loads
+    g = _by_name(compile_program(gpu_cases.attention_head(256, 64)))["matmul_O_fused"]
+    src = g.kernel.source
+    assert "ld_A_tile.template fetch_raw<false>(" in src
+    assert "ld_A_tile.template commit_xf<" in src
+    assert "ld_B_tile.template fetch<false>(" in src  # no transform on V
+
+
+def test_full_operand_prologue_is_applied_at_fetch():
+    # (h1 * s * h2) @ W3: s and h2 are full matrices, loaded with the A tile
+    g = _by_name(compile_program(gpu_cases.mlp_block(128, 128, 384)))["matmul_out_fused"]
+    src = g.kernel.source
+    assert "fetch_raw" not in src.split("extern \"C\"")[1]
+    assert "ld_A_tile.template fetch<false>(" in src and ", xf_A_tile);" in src
+
+
+def test_batched_tables_hold_global_pointers_and_compile():
+    groups = compile_program(gpu_cases.attention_head(128, 64), batch=4)
+    for g in groups:
+        k = g.kernel.batched()
+        body = k.source.split('extern "C"')[1]
+        assert "MT_GLOBAL float* const* __restrict__ g_" in body
+        assert "_tab[blockIdx.z];" in body
+        assert hip_backend.compile_only(k.source) > 0
+
+
+def test_persistent_loop_only_when_tiles_exceed_one_round(monkeypatch):
+    from metellus_amd.compute.matmul import config
+
+    gemm = compile_program(gpu_cases.plain_matmul(4096, 4096, 4096))[0]
+    assert gemm.grid == (16, 16, 1)  # 256 tiles of 256x256: one per CU
+    assert "mt_t += gridDim.x" not in gemm.kernel.source
+
+    monkeypatch.setattr(config, "PERSISTENT_CAPACITY", 2)
+    g = compile_program(gpu_cases.plain_matmul(192, 96, 320))[0]
+    assert g.grid == (2, 1, 1)
+    src = g.kernel.source
+    assert "for (unsigned mt_t = blockIdx.x; mt_t < mt_tiles; mt_t += gridDim.x) {" in src
+    assert "} else if (mt_has_next) {" in src and "}  // persistent tile loop" in src
+    assert hip_backend.compile_only(src) > 0
+
+
+def test_persistent_batched_grid_splits_capacity_over_programs(monkeypatch):
+    from metellus_amd.compute.matmul import config
+
+    monkeypatch.setattr(config, "PERSISTENT_CAPACITY", 8)
+    groups = compile_program(gpu_cases.attention_head(256, 64), batch=3)
+    s_kernel = groups[0]  # S = Q @ K^T, 256 x 256 output per program
+    assert s_kernel.grid == (8 // 3, 1, 1)  # 2 workgroups per program, 3 programs in grid z
+    assert hip_backend.compile_only(s_kernel.kernel.batched().source) > 0
+
+
+def test_persistent_switch_off_restores_classic_grid(monkeypatch):
+    from metellus_amd.compute.matmul import config
+
+    monkeypatch.setattr(config, "PERSISTENT_CAPACITY", 2)
+    monkeypatch.setattr(config, "PERSISTENT", False)
+    g = compile_program(gpu_cases.plain_matmul(192, 96, 320))[0]
+    assert g.grid[2] == 1 and g.grid[0] * g.grid[1] > 2

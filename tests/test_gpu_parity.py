@@ -195,6 +195,42 @@ def test_register_epilogue_and_prologue():
     _check_matmul(res.env["D"], a, ops.uploads["B"] * 0.25, evaluate(ops)["D"])
 
 
+@pytest.mark.parametrize("layout", ["rowmajor", "transposed", "transposed_odd"])
+def test_broadcast_prologues_applied_at_commit(layout):
+    """Prologues reading only broadcast operands are applied when the tile is
+    written to LDS (fetch_raw / commit_xf).  A is loaded 128-bit along
+    columns (row-major), 128-bit along rows (transposed view, column stride
+    100) or element by element (transposed view, column stride 101); B
+    (N = 90) by elements.  M, N are not tile multiples, so bounds apply."""
+    rng = np.random.default_rng(12)
+    M = 101 if layout == "transposed_odd" else 100
+    K, N = 72, 90
+    ops = Operations()
+    if layout == "rowmajor":
+        ops.from_numpy(rng.standard_normal((M, K)).astype(np.float32), "A")
+    else:
+        ops.from_numpy(rng.standard_normal((K, M)).astype(np.float32), "At")
+        ops.transpose("At", out="A")
+    ops.from_numpy(rng.standard_normal(M).astype(np.float32), "mu")
+    ops.from_numpy(rng.uniform(0.5, 1.5, K).astype(np.float32), "g")
+    ops.from_numpy(rng.standard_normal((K, N)).astype(np.float32), "B")
+    ops.from_numpy(rng.uniform(0.5, 1.5, N).astype(np.float32), "h")
+    ops.reshape("mu", (M, 1), out="mu_c")
+    ops.reshape("g", (1, K), out="g_r")
+    ops.reshape("h", (1, N), out="h_r")
+    ops.elementwise("subtract", out="a1", operands=("A", "mu_c"), y_broadcast="col")
+    ops.elementwise("mul", out="a2", operands=("a1", "g_r"), y_broadcast="row")
+    ops.elementwise("mul", out="b1", operands=("B", "h_r"), y_broadcast="row")
+    ops.matmul(a="a2", b="b1", out="C")
+    res = run(ops)
+    assert [g.strategy for g in res.groups] == [FusionStrategy.ELEMENTWISE_PROLOGUE_MATMUL]
+    src = res.groups[0].kernel.source
+    # A and B loaders, each once before the k loop and once inside it
+    assert src.count("fetch_raw<true>") == 4 and src.count("commit_xf<") == 4
+    ref = evaluate(ops)
+    _check_matmul(res.env["C"], ref["a2"], ref["b1"], ref["C"])
+
+
 def test_transposed_operands():
     rng = np.random.default_rng(4)
     ops = Operations()
@@ -247,8 +283,9 @@ def test_mlp_block_literal():
     np.testing.assert_allclose(res.env["out"], ref["out"], rtol=1e-3, atol=1e-4)
 
 
-def test_attention_head():
-    ops = gpu_cases.attention_head(256, 64)
+@pytest.mark.parametrize("S,Dh", [(256, 64), (100, 40)])
+def test_attention_head(S, Dh):
+    ops = gpu_cases.attention_head(S, Dh)
     res = run(ops)
     assert len(res.groups) == 5
     ref = evaluate(ops)
