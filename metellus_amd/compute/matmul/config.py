@@ -30,6 +30,7 @@ class TileConfig:
     a_pad: int = 4
     b_pad: int = 4
     stages: int = 2
+    c_pad: int = 4  # row padding of an LDS C tile (MatmulAccumToTgFragment)
 
     @property
     def num_threads(self) -> int:
@@ -78,8 +79,8 @@ class TileConfig:
             raise ValueError(f"wave tile must be a multiple of 32x32: {self}")
         if self.tile_K % 8:
             raise ValueError(f"tile_K must be a multiple of 8: {self}")
-        if self.lda % 4 or self.ldb % 4:
-            raise ValueError(f"LDS row pitch must be a multiple of 4 floats: {self}")
+        if self.lda % 4:
+            raise ValueError(f"A tile row pitch must be a multiple of 4 floats (128-bit reads): {self}")
         if self.num_threads > 1024:
             raise ValueError(f"at most 1024 lanes per workgroup: {self}")
 

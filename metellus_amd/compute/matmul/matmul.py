@@ -172,18 +172,20 @@ class MatmulComputeFragment:
     name: str = "matmul_compute"
     kind: str = "compute"
 
-    def render_stage(self, stage: str) -> str:
+    def render_stage(self, stage: str | None) -> str:
+        """MFMAs over LDS buffer ``stage`` of double-buffered tiles, or over
+        single-buffered tiles when ``stage`` is None."""
         t = self.config.tile
         at, bt = self.config.a_tile_name, self.config.b_tile_name
-        a_ptr = f"&{at}[{stage}][wave_m0][0]" if t.stages > 1 else f"&{at}[wave_m0][0]"
-        b_ptr = f"&{bt}[{stage}][0][wave_n0]" if t.stages > 1 else f"&{bt}[0][wave_n0]"
+        a_ptr = f"&{at}[{stage}][wave_m0][0]" if stage is not None else f"&{at}[wave_m0][0]"
+        b_ptr = f"&{bt}[{stage}][0][wave_n0]" if stage is not None else f"&{bt}[0][wave_n0]"
         return (
             f"mt_mfma_tile<{t.WM}, {t.WN}, {t.tile_K}, {t.lda}, {t.ldb}>"
             f"({a_ptr}, {b_ptr}, acc{self.accumulator_suffix}, lane);"
         )
 
     def render(self, ctx: CodegenContext) -> str:
-        return self.render_stage("0")
+        return self.render_stage("0" if self.config.tile.stages > 1 else None)
 
     @property
     def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
@@ -247,7 +249,7 @@ class MatmulMainloopFragment:
                 *[f"    {ld.render_fetch()}" for ld in loads],
                 *[f"    {ld.render_commit('0')}" for ld in loads],
                 "    __syncthreads();",
-                *[f"    {c.render_stage('0')}" for c in computes],
+                *[f"    {c.render_stage(None)}" for c in computes],
                 "    __syncthreads();",
                 "}",
             ]
@@ -386,6 +388,81 @@ class MatmulAccumToDevFragment:
 
 
 @dataclass(frozen=True)
+class MatmulAccumToTgFragment:
+    """Accumulators -> the LDS tile ``C_tile[tile_M][tile_N + c_pad]``
+    (reference: src/compute/matmul/matmul.py:270-313).  A barrier must follow
+    before the tile is read.  The kernels this package assembles keep
+    epilogues in registers and never stage C through LDS; this fragment and
+    ``MatmulTgToDevFragment`` serve hand-composed kernels."""
+
+    config: MatmulConfig
+    accumulator_suffix: str = ""
+    emit_tg_coords: bool = True
+    name: str = "matmul_accum_to_tg"
+    kind: str = "store"
+
+    def render(self, ctx: CodegenContext) -> str:
+        t = self.config.tile
+        c = self.config.c_tile_name
+        a = f"acc{self.accumulator_suffix}"
+        return "\n".join(
+            [
+                "#pragma unroll",
+                f"for (int i = 0; i < {t.WM}; ++i) {{",
+                "#pragma unroll",
+                f"    for (int j = 0; j < {t.WN}; ++j) {{",
+                "#pragma unroll",
+                "        for (int v = 0; v < 16; ++v) {",
+                f"            {c}[wave_m0 + (unsigned)i * 32u + mt_acc_row(v, lane)]"
+                f"[wave_n0 + (unsigned)j * 32u + (lane & 31u)] = {a}[i][j][v];",
+                "        }",
+                "    }",
+                "}",
+            ]
+        )
+
+    @property
+    def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
+        t = self.config.tile
+        shape = (t.tile_M, t.tile_N + t.c_pad)
+        return (TgmemAccess(self.config.c_tile_name, "write", _prod(shape), shape),)
+
+
+@dataclass(frozen=True)
+class MatmulTgToDevFragment:
+    """LDS ``C_tile`` -> the output, masked to (M, N) (reference:
+    src/compute/matmul/matmul.py:317-352)."""
+
+    config: MatmulConfig
+    name: str = "matmul_tg_to_dev"
+    kind: str = "store"
+
+    def render(self, ctx: CodegenContext) -> str:
+        from metellus_amd.memory.memory import TgStoreFragment
+
+        t = self.config.tile
+        return TgStoreFragment(
+            name="store_C_tile",
+            src_name=self.config.c_tile_name,
+            dst_name=self.config.c_buffer_name,
+            dst_row_stride=self.config.N_dim_var,
+            row_start="tile_m0",
+            col_start="tile_n0",
+            tile_shape=(t.tile_M, t.tile_N),
+            num_threads=t.num_threads,
+            row_limit=self.config.M_dim_var,
+            col_limit=self.config.N_dim_var,
+            dst_col_stride=self.config.c_col_stride,
+        ).render(ctx)
+
+    @property
+    def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
+        t = self.config.tile
+        shape = (t.tile_M, t.tile_N + t.c_pad)
+        return (TgmemAccess(self.config.c_tile_name, "read", _prod(shape), shape),)
+
+
+@dataclass(frozen=True)
 class MatmulRegisterEpilogueFragment:
     """Rewrite accumulators in place with ``value_transform`` (a closure over
     the register value expression), before a store fragment."""
@@ -420,6 +497,8 @@ class MatmulRegisterEpilogueFragment:
 
 __all__ = [
     "MatmulAccumToDevFragment",
+    "MatmulAccumToTgFragment",
+    "MatmulTgToDevFragment",
     "MatmulComputeFragment",
     "MatmulConfig",
     "MatmulEpilogueStoreFragment",

@@ -59,6 +59,22 @@ def _combine(op: str, a: str, b: str) -> str:
     raise ValueError(f"unsupported reduction op: {op}")
 
 
+def _mult4(v: str) -> bool:
+    try:
+        return int(v) % 4 == 0
+    except (TypeError, ValueError):
+        return False
+
+
+def _uint(v: str) -> str:
+    """An unsigned operand: integer literals get the ``u`` suffix, anything
+    else (a dim name or expression) is parenthesised."""
+    try:
+        return f"{int(v)}u"
+    except (TypeError, ValueError):
+        return f"({v})"
+
+
 def _check_op(op: str) -> None:
     if op not in REDUCTION_OPS:
         raise ValueError(f"unsupported reduction op: {op}")
@@ -132,9 +148,12 @@ class LastAxisReductionComputeFragment:
         return (TgmemAccess(self.scratch_name, "readwrite", n, (n,)),)
 
     def _vec(self) -> bool:
+        """128-bit loads need contiguous rows whose length and stride are
+        known multiples of 4 (the vector loop covers ``reduce_dim / 4``
+        quads and nothing else); symbolic sizes take the per-element loop."""
         if self.vectorized is not None:
             return self.vectorized
-        return self.col_stride == "1"
+        return self.col_stride == "1" and _mult4(self.reduce_dim) and _mult4(self.row_stride)
 
     def render(self, ctx: CodegenContext) -> str:
         _check_op(self.op)
@@ -143,7 +162,7 @@ class LastAxisReductionComputeFragment:
         ld4 = "mt_ld4_nt" if self.nt_load else "mt_ld4"
         ident = _identity(self.op)
         tf = self.value_transform or (lambda raw: raw)
-        src = f"{self.input_name} + (size_t)row * {self.row_stride}u"
+        src = f"{self.input_name} + (size_t)row * {_uint(self.row_stride)}"
         L = [f"float a0 = {ident}, a1 = {ident}, a2 = {ident}, a3 = {ident};", "if (row_ok) {",
              f"    const float* __restrict__ src = {src};"]
         if self._vec():
@@ -176,7 +195,7 @@ class LastAxisReductionComputeFragment:
             L += ["    }"]
         else:
             cs = self.col_stride
-            load = "src[idx]" if cs == "1" else f"src[(size_t)idx * {cs}u]"
+            load = "src[idx]" if cs == "1" else f"src[(size_t)idx * {_uint(cs)}]"
             L += [
                 "    unsigned e = t;",
                 f"    for (; e + {(U - 1) * T}u < {self.reduce_dim}; e += {U * T}u) {{",

@@ -125,15 +125,55 @@ struct mt_tile_colvec {
         }
     }
 
+    // Any row stride, limits and base alignment (the strides and limits are
+    // run-time values): a slot is loaded with one 128-bit load when its row
+    // start is 16-byte aligned and all 4 columns are in bounds, otherwise
+    // element by element (out-of-bounds elements are 0, and f is applied to
+    // in-bounds elements only).  Same register layout as fetch().
+    template <typename F>
+    MT_INLINE void fetch_safe(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
+                              unsigned rlim, unsigned clim, unsigned tid, F f) {
+        const bool aligned =
+            ((rs & 3u) == 0u) && ((reinterpret_cast<unsigned long long>(src) & 15ull) == 0ull) && ((col0 & 3u) == 0u);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / CV, c = (idx % CV) * 4u;
+            const unsigned gr = row0 + r, gc = col0 + c;
+            mt_f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && gr < rlim && gc < clim) {
+                const float* p = src + (size_t)gr * rs + gc;
+                if (aligned && gc + 3u < clim) {
+                    x = mt_ld4(p);
+                    x.x = f(x.x, gr, gc);
+                    x.y = f(x.y, gr, gc + 1u);
+                    x.z = f(x.z, gr, gc + 2u);
+                    x.w = f(x.w, gr, gc + 3u);
+                } else {
+                    x.x = f(p[0], gr, gc);
+                    if (gc + 1u < clim) x.y = f(p[1], gr, gc + 1u);
+                    if (gc + 2u < clim) x.z = f(p[2], gr, gc + 2u);
+                    if (gc + 3u < clim) x.w = f(p[3], gr, gc + 3u);
+                }
+            }
+            v[i] = x;
+        }
+    }
+
+    // 128-bit LDS stores when the row pitch keeps them 16-byte aligned.
     template <int LD>
     MT_INLINE void commit(float* lds, unsigned tid) const {
-        static_assert(LD % 4 == 0, "colvec commit needs a 16-byte row pitch");
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const unsigned idx = tid + i * NT;
             if (TOTAL % NT == 0 || idx < (unsigned)TOTAL) {
                 const unsigned r = idx / CV, c = (idx % CV) * 4u;
-                mt_st4(lds + r * LD + c, v[i]);
+                if constexpr (LD % 4 == 0) {
+                    mt_st4(lds + r * LD + c, v[i]);
+                } else {
+                    float* d = lds + r * LD + c;
+                    d[0] = v[i].x, d[1] = v[i].y, d[2] = v[i].z, d[3] = v[i].w;
+                }
             }
         }
     }

@@ -15,7 +15,17 @@ gfx950 choices (in ``mt_device.h``):
 * a load is split into ``fetch`` (global -> registers) and ``commit``
   (registers -> LDS) so a pipelined mainloop can keep the next tile's loads
   in flight during the MFMAs; LDS tiles may hold ``stages`` buffers and a
-  padded row pitch.
+  padded row pitch;
+* when the mode is not given, it is chosen from what the parameters prove:
+  128-bit loads without run-time checks need an integer row stride and
+  column limit that are multiples of 4; a contiguous row with a symbolic
+  stride or limit gets ``colvec_safe`` (128-bit where a run-time check shows
+  the 4 columns aligned and in bounds, else per element), as the reference
+  does (memory.py:277-286);
+* without ``dst_pitch`` the LDS row pitch is the declared array's
+  (``sizeof(dst[0]) / sizeof(float)``), so a padded declaration works;
+* lane index: ``threadIdx.x`` for one-dimensional workgroups, the flat
+  ``threadIdx.y * tg_x + threadIdx.x`` when the context has ``tg_y > 1``.
 
 The transform, when present, is rendered as a C++ lambda
 ``(float raw, unsigned global_row, unsigned global_col) -> float``; a
@@ -31,6 +41,16 @@ from typing import Callable
 from metellus_amd.compute.fragments import CodegenContext, TgmemAccess
 
 ValueTransform = Callable[[str], str]
+
+
+def flat_tid(ctx: CodegenContext) -> str:
+    """This lane's index within the workgroup."""
+    return f"(threadIdx.y * {ctx.tg_x}u + threadIdx.x)" if ctx.tg_y > 1 else "threadIdx.x"
+
+
+def _mult4(limit: str | None) -> bool:
+    """A bound that is absent or a literal multiple of 4."""
+    return limit is None or (_is_int(limit) and int(limit) % 4 == 0)
 
 
 def _is_int(s: str) -> bool:
@@ -68,8 +88,12 @@ class TgLoadFragment:
     defer_transform: bool = False
 
     @property
-    def pitch(self) -> int:
-        return self.dst_pitch if self.dst_pitch is not None else self.tile_shape[1]
+    def pitch(self) -> str:
+        """LDS row pitch in floats (a C++ constant expression)."""
+        if self.dst_pitch is not None:
+            return str(self.dst_pitch)
+        row = f"{self.dst_name}[0][0]" if self.stages > 1 else f"{self.dst_name}[0]"
+        return f"sizeof({row}) / sizeof(float)"
 
     @property
     def check(self) -> bool:
@@ -80,9 +104,11 @@ class TgLoadFragment:
             return self.mode
         rows, cols = self.tile_shape
         rs, cs = self.src_row_stride, self.src_col_stride
-        if cs == "1" and cols % 4 == 0 and self.pitch % 4 == 0 and (not _is_int(rs) or int(rs) % 4 == 0):
-            return "colvec"
-        if rs == "1" and rows % 4 == 0 and _is_int(cs) and int(cs) % 4 == 0:
+        pitch_ok = self.dst_pitch is None or self.dst_pitch % 4 == 0
+        if cs == "1" and cols % 4 == 0 and pitch_ok:
+            proven = _is_int(rs) and int(rs) % 4 == 0 and _mult4(self.col_limit)
+            return "colvec" if proven else "colvec_safe"
+        if rs == "1" and rows % 4 == 0 and _is_int(cs) and int(cs) % 4 == 0 and _mult4(self.row_limit):
             return "rowvec"
         return "scalar"
 
@@ -104,25 +130,29 @@ class TgLoadFragment:
 
     def render_decl(self) -> str:
         rows, cols = self.tile_shape
-        tmpl = {"colvec": "mt_tile_colvec", "rowvec": "mt_tile_rowvec", "scalar": "mt_tile_scalar"}[self.resolved_mode()]
+        tmpl = {"colvec": "mt_tile_colvec", "colvec_safe": "mt_tile_colvec", "rowvec": "mt_tile_rowvec",
+                "scalar": "mt_tile_scalar"}[self.resolved_mode()]
         return f"{tmpl}<{rows}, {cols}, {self.num_threads}> {self.loader};\nconst auto {self.xform} = {self._lambda()};"
 
-    def render_fetch(self) -> str:
+    def render_fetch(self, tid: str = "threadIdx.x") -> str:
         rlim = self.row_limit if self.row_limit is not None else "0xffffffffu"
         clim = self.col_limit if self.col_limit is not None else "0xffffffffu"
         check = "true" if self.check else "false"
         mode = self.resolved_mode()
-        deferred = self.defer_transform and self._has_transform()
-        verb = "fetch_raw" if deferred else "fetch"
-        head = f"{self.loader}.template {verb}<{check}>({self.src_name}, "
-        if mode == "colvec":
+        deferred = self.defer_transform and self._has_transform() and mode != "colvec_safe"
+        if mode == "colvec_safe":
+            head = f"{self.loader}.fetch_safe({self.src_name}, "
+        else:
+            verb = "fetch_raw" if deferred else "fetch"
+            head = f"{self.loader}.template {verb}<{check}>({self.src_name}, "
+        if mode in ("colvec", "colvec_safe"):
             strides = f"{self.src_row_stride}"
         elif mode == "rowvec":
             strides = f"{self.src_col_stride}"
         else:
             strides = f"{self.src_row_stride}, {self.src_col_stride}"
         tail = ")" if deferred else f", {self.xform})"
-        return f"{head}{strides}, {self.row_start}, {self.col_start}, {rlim}, {clim}, threadIdx.x{tail};"
+        return f"{head}{strides}, {self.row_start}, {self.col_start}, {rlim}, {clim}, {tid}{tail};"
 
     def _has_transform(self) -> bool:
         return self.transform_lambda is not None or self.value_transform is not None
@@ -132,22 +162,27 @@ class TgLoadFragment:
             return f"&{self.dst_name}[{stage}][0][0]"
         return f"&{self.dst_name}[0][0]"
 
-    def render_commit(self, stage: str = "0") -> str:
-        if self.defer_transform and self._has_transform():
+    def render_commit(self, stage: str = "0", tid: str = "threadIdx.x") -> str:
+        if self.defer_transform and self._has_transform() and self.resolved_mode() != "colvec_safe":
             check = "true" if self.check else "false"
             return (
                 f"{self.loader}.template commit_xf<{self.pitch}, {check}>"
-                f"({self.stage_ptr(stage)}, threadIdx.x, {self.xform});"
+                f"({self.stage_ptr(stage)}, {tid}, {self.xform});"
             )
-        return f"{self.loader}.template commit<{self.pitch}>({self.stage_ptr(stage)}, threadIdx.x);"
+        return f"{self.loader}.template commit<{self.pitch}>({self.stage_ptr(stage)}, {tid});"
 
     def render(self, ctx: CodegenContext) -> str:
-        return "{\n" + "\n".join([self.render_decl(), self.render_fetch(), self.render_commit("0")]) + "\n}"
+        tid = flat_tid(ctx)
+        return "{\n" + "\n".join([self.render_decl(), self.render_fetch(tid), self.render_commit("0", tid)]) + "\n}"
 
     @property
     def lds_shape(self) -> tuple[int, ...]:
-        rows = self.tile_shape[0]
-        return (self.stages, rows, self.pitch) if self.stages > 1 else (rows, self.pitch)
+        """Shape of the LDS region written: the padded rows when the pitch is
+        given, else the logical tile (the declaration's padding, if any, is
+        not known here)."""
+        rows, cols = self.tile_shape
+        width = self.dst_pitch if self.dst_pitch is not None else cols
+        return (self.stages, rows, width) if self.stages > 1 else (rows, width)
 
     @property
     def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
@@ -184,7 +219,7 @@ class TgStoreFragment:
             store = f"if (gr < ({self.row_limit}) && gc < ({self.col_limit})) {{ {store} }}"
         return "\n".join(
             [
-                f"for (unsigned idx = threadIdx.x; idx < {rows * cols}u; idx += {self.num_threads}u) {{",
+                f"for (unsigned idx = {flat_tid(ctx)}; idx < {rows * cols}u; idx += {self.num_threads}u) {{",
                 f"    const unsigned r = idx / {cols}u, c = idx % {cols}u;",
                 f"    const unsigned gr = ({self.row_start}) + r, gc = ({self.col_start}) + c;",
                 f"    {store}",

@@ -17,6 +17,8 @@ outnumber the workgroups resident at once, the grid is instead
 
 from __future__ import annotations
 
+import dataclasses
+
 from metellus_amd.compute.fragments import BarrierFragment, CodegenContext, lds_decl
 from metellus_amd.compute.matmul.config import (
     TileConfig,
@@ -72,7 +74,7 @@ def operand_load(
         row_start, col_start = "k_chunk", "tile_n0"
         row_lim, col_lim = k_limit, "N"
         rows_total, cols_total = K, N
-    if cs == 1 and rs % 4 == 0 and cols_total % 4 == 0:
+    if cs == 1 and rs % 4 == 0 and cols_total % 4 == 0 and pitch % 4 == 0:
         mode = "colvec"
     elif rs == 1 and cs % 4 == 0 and rows_total % 4 == 0:
         mode = "rowvec"
@@ -99,6 +101,19 @@ def operand_load(
     )
 
 
+def b_tile_for(tile: TileConfig, src_b: Tensor, K: int, N: int) -> TileConfig:
+    """Row pitch of the B tile in LDS.  A B operand read 128-bit along
+    columns is committed with 128-bit stores and keeps a pitch that is a
+    multiple of 4 floats.  Any other B (a transposed view such as K^T, or
+    odd strides) is committed by 32-bit stores walking down columns, where a
+    pitch of tile_N + 4 puts rows 0, 4, 8, ... of a column on colliding
+    banks; an odd pitch (tile_N + 3) spreads them (measured on MI355X for
+    the attention S = Q @ K^T kernel: 372.8 -> 360.5 us)."""
+    if src_b.col_stride == 1 and src_b.row_stride % 4 == 0 and N % 4 == 0:
+        return tile
+    return dataclasses.replace(tile, b_pad=3)
+
+
 def assemble_matmul(decision: DecisionView, function_name: str | None, batch: int = 1) -> KernelGroup:
     anchor = decision.anchor
     assert isinstance(anchor, MatmulOp)
@@ -107,7 +122,7 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
     assert isinstance(src_a, Tensor) and isinstance(src_b, Tensor)
     M, K = anchor.a.shape
     N = anchor.b.shape[1]
-    tile = select_tile_config(M, K, N, batch=batch)
+    tile = b_tile_for(select_tile_config(M, K, N, batch=batch), src_b, K, N)
     aligned = is_aligned_shape(M, K, N, tile)
     final_out = decision.epilogue[-1].out if decision.epilogue else anchor.out
     out_key = final_out.buffer_key

@@ -29,7 +29,7 @@ from metellus_amd.compute.matmul.matmul import (
 from metellus_amd.orchestrator.assembly.decision import DecisionView
 from metellus_amd.orchestrator.assembly.expressions import ChainCode
 from metellus_amd.orchestrator.assembly.extras import Extras, input_param, output_param, param_name
-from metellus_amd.orchestrator.assembly.matmul import operand_load
+from metellus_amd.orchestrator.assembly.matmul import b_tile_for, operand_load
 from metellus_amd.orchestrator.ir import Tensor
 from metellus_amd.orchestrator.kernel_group import KernelGroup
 from metellus_amd.runtime.program import Kernel
@@ -51,6 +51,9 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
     assert all(isinstance(t, Tensor) for t in (*src_a, *src_b))
     out_key = merge.out.buffer_key
     tile = select_tile_config(M, max(K0, K1), N, anchors=2, batch=batch)
+    padded = [b_tile_for(tile, src_b[i], (K0, K1)[i], N) for i in range(2)]
+    if all(p.b_pad != tile.b_pad for p in padded):
+        tile = padded[0]  # both B tiles committed by 32-bit stores
     aligned = is_aligned_shape(M, K0, N, tile) and is_aligned_shape(M, K1, N, tile)
 
     order = (src_a[0], src_b[0], src_b[1]) if shared else (src_a[0], src_b[0], src_a[1], src_b[1])
