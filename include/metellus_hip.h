@@ -65,6 +65,16 @@ int mt_read(uint64_t handle, void* dst, size_t nbytes);
 /* fill_buffer (reference: src/metal_backend.mm:128-141): byte fill. */
 int mt_fill(uint64_t handle, uint8_t value);
 
+/* Page-locked host memory of at least nbytes (no counterpart in the
+ * reference, whose buffers are unified memory).  Reads into it run at the
+ * link's DMA rate with no staging copy; the Python wrapper backs large
+ * downloads with it.  Blocks come from a pool (64 KiB granules) and return
+ * to it on mt_host_free; up to 1 GiB of returned blocks stay cached. */
+int mt_host_alloc(size_t nbytes, void** ptr);
+
+/* Return a block from mt_host_alloc to the pool (NULL is a no-op). */
+int mt_host_free(void* ptr);
+
 /* First half of run_kernel (reference: src/metal_backend.mm:178-207):
  * compile `source` with hiprtc for the device's target, load it and look up
  * `function_name`.  Code objects are cached in memory (and on disk unless

@@ -8,6 +8,8 @@ passed as per-program pointer tables), instead of once per program."""
 
 from __future__ import annotations
 
+from collections.abc import Iterable
+
 from typing import Any, NamedTuple
 
 import numpy as np
@@ -31,11 +33,13 @@ def compile_program(ops: Operations, *, batch: int = 1) -> tuple[KernelGroup, ..
     return tuple(alias_group(assemble(v, batch=batch)) for v in fuse(ops.build()))
 
 
-def run(ops: Operations, *, profile: bool = False) -> RunResult:
+def run(ops: Operations, *, profile: bool = False, outputs: Iterable[str] | None = None) -> RunResult:
     """Compile and execute; outputs land in ``env`` under their tensor names
-    (``profile=True`` adds per-kernel GPU ms as ``t_0``, ``t_1``, ...)."""
+    (``profile=True`` adds per-kernel GPU ms as ``t_0``, ``t_1``, ...).
+    ``outputs`` limits the downloads to those names (every materialised
+    tensor otherwise, as in the reference)."""
     groups = compile_program(ops)
-    runtime = schedule(ops, groups, profile=profile)
+    runtime = schedule(ops, groups, profile=profile, outputs=outputs)
     return RunResult(env=runtime.run(), groups=groups)
 
 
@@ -62,10 +66,15 @@ class BatchRunner:
     """Executes the schedules of ``len(programs)`` structurally identical
     programs in lockstep; every Dispatch is one batched launch."""
 
-    def __init__(self, programs: list[Operations], *, profile: bool = False) -> None:
+    def __init__(
+        self, programs: list[Operations], *, profile: bool = False, outputs: Iterable[str] | None = None
+    ) -> None:
         self.programs = list(programs)
         self.groups = [compile_program(ops, batch=len(self.programs)) for ops in self.programs]
-        self.plans = [schedule(ops, g, profile=profile) for ops, g in zip(self.programs, self.groups)]
+        outputs = None if outputs is None else tuple(outputs)
+        self.plans = [
+            schedule(ops, g, profile=profile, outputs=outputs) for ops, g in zip(self.programs, self.groups)
+        ]
         self.batched = len(self.programs) > 1 and _same_plan(self.plans)
 
     def run(self) -> list[RunResult]:
@@ -105,8 +114,11 @@ class BatchRunner:
         return [RunResult(env=e, groups=g) for e, g in zip(envs, self.groups)]
 
 
-def run_batch(programs: list[Operations], *, profile: bool = False) -> list[RunResult]:
+def run_batch(
+    programs: list[Operations], *, profile: bool = False, outputs: Iterable[str] | None = None
+) -> list[RunResult]:
     """Run structurally identical programs with one launch per fused kernel
     for the whole batch (falls back to one run per program when their plans
-    differ).  With ``profile`` each env gets the batched launch time."""
-    return BatchRunner(programs, profile=profile).run()
+    differ).  With ``profile`` each env gets the batched launch time;
+    ``outputs`` limits the downloads as in ``run``."""
+    return BatchRunner(programs, profile=profile, outputs=outputs).run()

@@ -20,6 +20,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <sys/stat.h>
@@ -76,7 +77,15 @@ struct State {
     std::unordered_map<std::string, uint64_t> by_key;  // exact key -> handle
     uint64_t compiled = 0;
     uint64_t hits = 0;
+    // Pinned host blocks: capacity of every live or cached block, and the
+    // cached (returned) ones by capacity.
+    std::unordered_map<void*, size_t> host_cap;
+    std::multimap<size_t, void*> host_free;
+    size_t host_cached = 0;
 };
+
+constexpr size_t kHostGranule = size_t(64) << 10;     // pinned blocks are multiples of 64 KiB
+constexpr size_t kHostCacheLimit = size_t(1) << 30;   // at most 1 GiB of returned blocks kept
 
 State& state() {
     static State s;
@@ -101,6 +110,14 @@ int init_locked(State& s) {
     MT_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
     MT_HIP(hipEventCreate(&s.ev_start));
     MT_HIP(hipEventCreate(&s.ev_stop));
+    // Keep memory released by hipFreeAsync in the device's pool instead of
+    // returning it at each synchronisation, so buffers of repeated runs are
+    // served from the pool.
+    hipMemPool_t pool = nullptr;
+    if (hipDeviceGetDefaultMemPool(&pool, 0) == hipSuccess && pool != nullptr) {
+        uint64_t keep = ~uint64_t(0);
+        MT_HIP(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep));
+    }
     s.ready = true;
     return 0;
 }
@@ -321,6 +338,45 @@ int mt_read(uint64_t handle, void* dst, size_t nbytes) {
     if (nbytes == 0) return 0;
     MT_HIP(hipMemcpyAsync(dst, b.ptr, nbytes, hipMemcpyDeviceToHost, s.stream));
     MT_HIP(hipStreamSynchronize(s.stream));
+    return 0;
+}
+
+int mt_host_alloc(size_t nbytes, void** ptr) {
+    if (!ptr) return fail("mt_host_alloc: null output");
+    if (nbytes == 0) return fail("mt_host_alloc: nbytes must be > 0");
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    const size_t want = (nbytes + kHostGranule - 1) / kHostGranule * kHostGranule;
+    // Reuse the smallest cached block that fits without wasting more than half.
+    auto it = s.host_free.lower_bound(want);
+    if (it != s.host_free.end() && it->first <= 2 * want) {
+        *ptr = it->second;
+        s.host_cached -= it->first;
+        s.host_free.erase(it);
+        return 0;
+    }
+    void* p = nullptr;
+    MT_HIP(hipHostMalloc(&p, want, hipHostMallocDefault));
+    s.host_cap.emplace(p, want);
+    *ptr = p;
+    return 0;
+}
+
+int mt_host_free(void* ptr) {
+    if (!ptr) return 0;
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    auto it = s.host_cap.find(ptr);
+    if (it == s.host_cap.end()) return fail("mt_host_free: pointer was not returned by mt_host_alloc");
+    const size_t cap = it->second;
+    if (s.host_cached + cap <= kHostCacheLimit) {
+        s.host_free.emplace(cap, ptr);
+        s.host_cached += cap;
+        return 0;
+    }
+    s.host_cap.erase(it);
+    MT_HIP(hipHostFree(ptr));
     return 0;
 }
 

@@ -18,6 +18,8 @@ Frees are stream-ordered in the native shim, so they need no host sync.
 
 from __future__ import annotations
 
+from collections.abc import Iterable
+
 import numpy as np
 
 from metellus_amd.orchestrator.builder import Operations
@@ -26,7 +28,17 @@ from metellus_amd.orchestrator.kernel_group import KernelGroup
 from metellus_amd.runtime.program import Allocate, Dispatch, Download, Free, FromNumpy, Runtime
 
 
-def schedule(ops: Operations, groups: tuple[KernelGroup, ...], *, profile: bool = False) -> Runtime:
+def schedule(
+    ops: Operations,
+    groups: tuple[KernelGroup, ...],
+    *,
+    profile: bool = False,
+    outputs: Iterable[str] | None = None,
+) -> Runtime:
+    """``outputs`` (an extension; the reference always downloads every
+    materialised tensor): download only these names and free every other
+    buffer at its last use.  A name that no kernel materialises -- an
+    intermediate fused into a kernel -- is an error."""
     program = ops.build()
     dag = build_dag(program)
     tensors = ops.tensors
@@ -48,9 +60,18 @@ def schedule(ops: Operations, groups: tuple[KernelGroup, ...], *, profile: bool 
     live_keys = set(input_keys)
     for g in groups:
         live_keys.update(g.bindings)
+    wanted: set[str] | None = None
+    if outputs is not None:
+        wanted = set(outputs)
+        unknown = sorted(n for n in wanted if n not in tensors)
+        if unknown:
+            raise ValueError(f"schedule: unknown output names {unknown}")
+        absent = sorted(n for n in wanted if n in uploads or tensors[n].buffer_key not in live_keys)
+        if absent:
+            raise ValueError(f"schedule: outputs {absent} are program inputs or not materialised by any kernel")
     names_by_key: dict[str, list[str]] = {}
     for name, t in tensors.items():
-        if name not in uploads and t.buffer_key in live_keys:
+        if name not in uploads and t.buffer_key in live_keys and (wanted is None or name in wanted):
             names_by_key.setdefault(t.buffer_key, []).append(name)
 
     last_use: dict[str, int] = {}

@@ -63,7 +63,13 @@ class Buffer:
         return out
 
     def numpy(self, shape: tuple[int, ...], dtype) -> np.ndarray:
-        return self.read_into(np.empty(shape, dtype=dtype))
+        """Download into a new array (page-locked from the pinned pool when
+        it is at least ``PINNED_MIN_BYTES``)."""
+        from metellus_amd.runtime.host import PINNED_MIN_BYTES, pinned_empty
+
+        nbytes = int(np.prod(shape, dtype=np.int64)) * np.dtype(dtype).itemsize
+        out = pinned_empty(shape, dtype) if nbytes >= PINNED_MIN_BYTES else np.empty(shape, dtype=dtype)
+        return self.read_into(out)
 
     def fill(self, byte_value: int) -> None:
         if not 0 <= byte_value <= 255:

@@ -39,6 +39,8 @@ EXPORTED_SYMBOLS = (
     "mt_write",
     "mt_read",
     "mt_fill",
+    "mt_host_alloc",
+    "mt_host_free",
     "mt_compile",
     "mt_compile_only",
     "mt_launch",
@@ -85,6 +87,8 @@ def _load():
             "mt_write": ([_u64, ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int),
             "mt_read": ([_u64, ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int),
             "mt_fill": ([_u64, ctypes.c_uint8], ctypes.c_int),
+            "mt_host_alloc": ([ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)], ctypes.c_int),
+            "mt_host_free": ([ctypes.c_void_p], ctypes.c_int),
             "mt_compile": ([ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_u64)], ctypes.c_int),
             "mt_compile_only": (
                 [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_size_t)],
@@ -192,6 +196,17 @@ def read_buffer(handle, out: np.ndarray) -> None:
     if not out.flags["C_CONTIGUOUS"]:
         raise ValueError("read_buffer: destination must be C-contiguous")
     _check(_load().mt_read(_handle_of(handle), out.ctypes.data_as(ctypes.c_void_p), out.nbytes))
+
+
+def host_alloc(nbytes: int) -> int:
+    """Page-locked host memory (pooled); returns its address."""
+    p = ctypes.c_void_p(0)
+    _check(_load().mt_host_alloc(int(nbytes), ctypes.byref(p)))
+    return int(p.value)
+
+
+def host_free(address: int) -> None:
+    _check(_load().mt_host_free(ctypes.c_void_p(int(address))))
 
 
 def fill_buffer(handle, value: int) -> None:

@@ -6,10 +6,11 @@ and freed after their last reader, transposed views download exactly."""
 import numpy as np
 import pytest
 
-from metellus_amd.api import compile_program
+from metellus_amd.api import compile_program, run
 from metellus_amd.orchestrator import Operations
 from metellus_amd.orchestrator.scheduler import schedule
-from oracle.ir_eval import matmul_tolerance
+from oracle.ir_eval import evaluate, matmul_tolerance
+from tests import gpu_cases
 
 pytestmark = pytest.mark.gpu
 
@@ -131,3 +132,34 @@ def test_kernel_cache_hits_on_repeat():
         schedule(ops, compile_program(ops)).run()
     after = hip_backend.cache_stats()
     assert after[0] == before[0]  # second run compiled nothing new
+
+
+def test_large_downloads_land_in_pinned_pool_memory():
+    import ctypes
+
+    from metellus_amd.runtime.host import PINNED_MIN_BYTES
+
+    ops = gpu_cases.sigmoid_chain(1024, 1024)  # 4 MiB output
+    first = run(ops).env["out"]
+    base = first.base
+    while base is not None and not isinstance(base, ctypes.Array):
+        base = getattr(base, "base", None)
+    assert isinstance(base, ctypes.Array) and first.nbytes >= PINNED_MIN_BYTES
+    ref = evaluate(ops)["out"]
+    np.testing.assert_allclose(first, ref, rtol=1e-5, atol=1e-5)
+    kept = first.copy()
+    # blocks go back to the pool and are reused; earlier results stay intact
+    for _ in range(3):
+        again = run(ops).env["out"]
+        np.testing.assert_array_equal(again, kept)
+    np.testing.assert_array_equal(first, kept)
+    del first, again
+    np.testing.assert_array_equal(run(ops).env["out"], kept)
+
+
+def test_outputs_selects_downloads():
+    ops = gpu_cases.softmax(64, 256)
+    full = run(ops).env
+    only = run(ops, outputs=["p"]).env
+    assert set(only) == {"p"}
+    np.testing.assert_array_equal(only["p"], full["p"])

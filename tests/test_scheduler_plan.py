@@ -10,6 +10,7 @@ from orchestrator.aliasing import alias_group
 from orchestrator.assembly import assemble
 from orchestrator.fusion import fuse
 from orchestrator.scheduler import schedule
+from metellus_amd.api import compile_program
 from runtime import Allocate, Dispatch, Download, Free, FromNumpy, Kernel
 
 
@@ -111,3 +112,31 @@ def test_view_of_produced_buffer_needs_no_upload():
     ops.elementwise("div", out="p", operands=("X", "sv"), y_broadcast="col")
     rt = schedule(ops, _groups(ops))
     assert [s.name for s in rt.fragments if isinstance(s, FromNumpy)] == ["X"]
+
+
+def test_outputs_limits_downloads_and_frees_the_rest():
+    from tests.gpu_cases import softmax
+
+    ops = softmax(32, 100)
+    groups = compile_program(ops)
+    full = schedule(ops, groups).fragments
+    only = schedule(ops, groups, outputs=["p"]).fragments
+    downloaded = lambda steps: sorted(f.into for f in steps if isinstance(f, Download))  # noqa: E731
+    freed = lambda steps: sorted(f.name for f in steps if isinstance(f, Free))  # noqa: E731
+    assert "p" in downloaded(full) and len(downloaded(full)) > 1
+    assert downloaded(only) == ["p"]
+    # every other produced buffer is freed at its last use instead
+    assert set(freed(only)) >= {g.bindings[-1] for g in groups if g.bindings[-1] != "p"} - set(ops.uploads)
+
+
+def test_outputs_must_be_materialised():
+    import pytest
+
+    from tests.gpu_cases import sigmoid_chain
+
+    ops = sigmoid_chain(16, 16)
+    groups = compile_program(ops)
+    with pytest.raises(ValueError, match="not materialised"):
+        schedule(ops, groups, outputs=["t1"])  # fused into the chain kernel
+    with pytest.raises(ValueError, match="unknown output"):
+        schedule(ops, groups, outputs=["nope"])
