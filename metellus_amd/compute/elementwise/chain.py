@@ -189,6 +189,22 @@ class ChainCode:
         """Call with every external fetched by a scalar load at (row, col)."""
         return self.call(seed_values, [e.scalar_fetch(row, col) for e in self.externals])
 
+    def gather_lambda(self, row: str = "global_row", col: str = "global_col") -> str:
+        """``[=](unsigned row, unsigned col) -> mt_vals<E>``: this element's
+        external operands, loaded with the tile (gather / apply loaders)."""
+        n = len(self.externals)
+        loads = " ".join(f"o.v[{k}] = {e.scalar_fetch(row, col)};" for k, e in enumerate(self.externals))
+        return f"[=](unsigned {row}, unsigned {col}) -> mt_vals<{n}> {{ mt_vals<{n}> o; {loads} return o; }}"
+
+    def apply_lambda(self) -> str:
+        """``[=](float raw, const mt_vals<E>& e) -> float``: the chain over a
+        loaded element and its gathered operands."""
+        n = len(self.externals)
+        return (
+            f"[=](float raw, const mt_vals<{n}>& e) -> float "
+            f"{{ return {self.call(['raw'], [f'e.v[{k}]' for k in range(n)])}; }}"
+        )
+
     def lambda_transform(self, row: str = "global_row", col: str = "global_col") -> str:
         """``[=](float raw, unsigned row, unsigned col) -> float`` applying the
         chain to a loaded element (matmul / reduction prologues)."""

@@ -14,6 +14,9 @@
 //                             fetch_raw + commit_xf apply the transform at
 //                             commit time instead, so the global loads stay
 //                             in flight across the MFMAs of the current chunk
+//   * mt_tile_*_g             the same loaders with fetch_gather/commit_apply:
+//                             a prologue's full-size operands are loaded with
+//                             the tile, the chain is applied at commit
 //   * MT_GLOBAL               global address space qualifier (pointer tables
 //                             of batched kernels hold global pointers, which
 //                             keeps their loads global_load, not flat_load)
@@ -334,6 +337,150 @@ struct mt_tile_scalar {
             }
         }
         commit<LD>(lds, tid);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Gather / apply loaders: a prologue that reads E full-size operands loads
+// them together with the tile (fetch_gather: g(row, col) -> mt_vals<E> per
+// element) and applies the chain when the tile is committed to LDS
+// (commit_apply: a(raw, extras) per in-bounds element), so neither the tile
+// nor its operands are waited for before the current chunk's MFMAs.  Out of
+// bounds elements stay 0 and are not transformed.
+// ---------------------------------------------------------------------------
+
+template <int E>
+struct mt_vals {
+    float v[E];
+};
+
+template <int ROWS, int COLS, int NT, int E>
+struct mt_tile_colvec_g : mt_tile_colvec<ROWS, COLS, NT> {
+    using Base = mt_tile_colvec<ROWS, COLS, NT>;
+    using Base::CV;
+    using Base::PER;
+    using Base::TOTAL;
+    mt_vals<E> ex[PER][4];
+
+    template <bool CHECK, typename G>
+    MT_INLINE void fetch_gather(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
+                                unsigned rlim, unsigned clim, unsigned tid, G g) {
+        this->r0 = row0, this->c0 = col0, this->rl = rlim, this->cl = clim;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / CV, c = (idx % CV) * 4u;
+            const unsigned gr = row0 + r, gc = col0 + c;
+            mt_f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rlim && gc < clim))) {
+                x = mt_ld4(src + (size_t)gr * rs + gc);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) ex[i][j] = g(gr, gc + (unsigned)j);
+            }
+            this->v[i] = x;
+        }
+    }
+
+    template <int LD, bool CHECK, typename A>
+    MT_INLINE void commit_apply(float* lds, unsigned tid, A a) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / CV, c = (idx % CV) * 4u;
+            const unsigned gr = this->r0 + r, gc = this->c0 + c;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < this->rl && gc < this->cl))) {
+                this->v[i].x = a(this->v[i].x, ex[i][0]);
+                this->v[i].y = a(this->v[i].y, ex[i][1]);
+                this->v[i].z = a(this->v[i].z, ex[i][2]);
+                this->v[i].w = a(this->v[i].w, ex[i][3]);
+            }
+        }
+        Base::template commit<LD>(lds, tid);
+    }
+};
+
+template <int ROWS, int COLS, int NT, int E>
+struct mt_tile_rowvec_g : mt_tile_rowvec<ROWS, COLS, NT> {
+    using Base = mt_tile_rowvec<ROWS, COLS, NT>;
+    using Base::RV;
+    using Base::PER;
+    using Base::TOTAL;
+    mt_vals<E> ex[PER][4];
+
+    template <bool CHECK, typename G>
+    MT_INLINE void fetch_gather(const float* __restrict__ src, unsigned cs, unsigned row0, unsigned col0,
+                                unsigned rlim, unsigned clim, unsigned tid, G g) {
+        this->r0 = row0, this->c0 = col0, this->rl = rlim, this->cl = clim;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned c = idx / RV, r = (idx % RV) * 4u;
+            const unsigned gr = row0 + r, gc = col0 + c;
+            mt_f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rlim && gc < clim))) {
+                x = mt_ld4(src + gr + (size_t)gc * cs);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) ex[i][j] = g(gr + (unsigned)j, gc);
+            }
+            this->v[i] = x;
+        }
+    }
+
+    template <int LD, bool CHECK, typename A>
+    MT_INLINE void commit_apply(float* lds, unsigned tid, A a) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned c = idx / RV, r = (idx % RV) * 4u;
+            const unsigned gr = this->r0 + r, gc = this->c0 + c;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < this->rl && gc < this->cl))) {
+                this->v[i].x = a(this->v[i].x, ex[i][0]);
+                this->v[i].y = a(this->v[i].y, ex[i][1]);
+                this->v[i].z = a(this->v[i].z, ex[i][2]);
+                this->v[i].w = a(this->v[i].w, ex[i][3]);
+            }
+        }
+        Base::template commit<LD>(lds, tid);
+    }
+};
+
+template <int ROWS, int COLS, int NT, int E>
+struct mt_tile_scalar_g : mt_tile_scalar<ROWS, COLS, NT> {
+    using Base = mt_tile_scalar<ROWS, COLS, NT>;
+    using Base::PER;
+    using Base::TOTAL;
+    mt_vals<E> ex[PER];
+
+    template <bool CHECK, typename G>
+    MT_INLINE void fetch_gather(const float* __restrict__ src, unsigned rs, unsigned cs, unsigned row0,
+                                unsigned col0, unsigned rlim, unsigned clim, unsigned tid, G g) {
+        this->r0 = row0, this->c0 = col0, this->rl = rlim, this->cl = clim;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / COLS, c = idx % COLS;
+            const unsigned gr = row0 + r, gc = col0 + c;
+            float x = 0.f;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rlim && gc < clim))) {
+                x = src[(size_t)gr * rs + (size_t)gc * cs];
+                ex[i] = g(gr, gc);
+            }
+            this->v[i] = x;
+        }
+    }
+
+    template <int LD, bool CHECK, typename A>
+    MT_INLINE void commit_apply(float* lds, unsigned tid, A a) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / COLS, c = idx % COLS;
+            const unsigned gr = this->r0 + r, gc = this->c0 + c;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < this->rl && gc < this->cl))) {
+                this->v[i] = a(this->v[i], ex[i]);
+            }
+        }
+        Base::template commit<LD>(lds, tid);
     }
 };
 

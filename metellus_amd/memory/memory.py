@@ -86,6 +86,12 @@ class TgLoadFragment:
     # next chunk's loads before its MFMAs.  Worth it when the transform reads
     # only small broadcast operands (those loads then happen at commit).
     defer_transform: bool = False
+    # Gather / apply: the transform's external operands are loaded with the
+    # tile (``gather_lambda``: (row, col) -> mt_vals<n_gathered>) and the
+    # chain (``apply_lambda``: (raw, operands) -> float) runs at commit.
+    gather_lambda: str | None = None
+    apply_lambda: str | None = None
+    n_gathered: int = 0
 
     @property
     def pitch(self) -> str:
@@ -128,10 +134,23 @@ class TgLoadFragment:
             return f"[=](float raw, unsigned global_row, unsigned global_col) -> float {{ return {expr}; }}"
         return "mt_identity{}"
 
+    @property
+    def gathering(self) -> bool:
+        return self.gather_lambda is not None
+
     def render_decl(self) -> str:
         rows, cols = self.tile_shape
+        mode = self.resolved_mode()
         tmpl = {"colvec": "mt_tile_colvec", "colvec_safe": "mt_tile_colvec", "rowvec": "mt_tile_rowvec",
-                "scalar": "mt_tile_scalar"}[self.resolved_mode()]
+                "scalar": "mt_tile_scalar"}[mode]
+        if self.gathering:
+            if mode == "colvec_safe" or self.apply_lambda is None or self.n_gathered < 1:
+                raise ValueError(f"{self.name}: gather/apply needs a proven load mode and an apply lambda")
+            return (
+                f"{tmpl}_g<{rows}, {cols}, {self.num_threads}, {self.n_gathered}> {self.loader};\n"
+                f"const auto xg_{self.dst_name} = {self.gather_lambda};\n"
+                f"const auto xa_{self.dst_name} = {self.apply_lambda};"
+            )
         return f"{tmpl}<{rows}, {cols}, {self.num_threads}> {self.loader};\nconst auto {self.xform} = {self._lambda()};"
 
     def render_fetch(self, tid: str = "threadIdx.x") -> str:
@@ -140,7 +159,10 @@ class TgLoadFragment:
         check = "true" if self.check else "false"
         mode = self.resolved_mode()
         deferred = self.defer_transform and self._has_transform() and mode != "colvec_safe"
-        if mode == "colvec_safe":
+        if self.gathering:
+            head = f"{self.loader}.template fetch_gather<{check}>({self.src_name}, "
+            deferred = False
+        elif mode == "colvec_safe":
             head = f"{self.loader}.fetch_safe({self.src_name}, "
         else:
             verb = "fetch_raw" if deferred else "fetch"
@@ -151,7 +173,10 @@ class TgLoadFragment:
             strides = f"{self.src_col_stride}"
         else:
             strides = f"{self.src_row_stride}, {self.src_col_stride}"
-        tail = ")" if deferred else f", {self.xform})"
+        if self.gathering:
+            tail = f", xg_{self.dst_name})"
+        else:
+            tail = ")" if deferred else f", {self.xform})"
         return f"{head}{strides}, {self.row_start}, {self.col_start}, {rlim}, {clim}, {tid}{tail};"
 
     def _has_transform(self) -> bool:
@@ -163,6 +188,12 @@ class TgLoadFragment:
         return f"&{self.dst_name}[0][0]"
 
     def render_commit(self, stage: str = "0", tid: str = "threadIdx.x") -> str:
+        if self.gathering:
+            check = "true" if self.check else "false"
+            return (
+                f"{self.loader}.template commit_apply<{self.pitch}, {check}>"
+                f"({self.stage_ptr(stage)}, {tid}, xa_{self.dst_name});"
+            )
         if self.defer_transform and self._has_transform() and self.resolved_mode() != "colvec_safe":
             check = "true" if self.check else "false"
             return (

@@ -80,7 +80,8 @@ def operand_load(
         mode = "rowvec"
     else:
         mode = "scalar"
-    lam = prologue.lambda_transform() if prologue is not None else None
+    gather = prologue is not None and not prologue.broadcast_operands_only and GATHER_PROLOGUES
+    lam = prologue.lambda_transform() if prologue is not None and not gather else None
     return TgLoadFragment(
         name=name,
         src_name=param_name(src.buffer_key),
@@ -98,7 +99,21 @@ def operand_load(
         mode=mode,
         transform_lambda=lam,
         defer_transform=prologue is not None and prologue.broadcast_operands_only,
+        gather_lambda=prologue.gather_lambda() if gather else None,
+        apply_lambda=prologue.apply_lambda() if gather else None,
+        n_gathered=len(prologue.externals) if gather else 0,
     )
+
+
+# Prologues that read full-size operands load them with the tile and apply
+# the chain at commit (gather / apply), on k-chunks of GATHER_TILE_K so the
+# extra registers fit beside a 256x256 tile's accumulators.
+GATHER_PROLOGUES = True
+GATHER_TILE_K = 16
+
+
+def gathers(prologue: ChainCode | None) -> bool:
+    return GATHER_PROLOGUES and prologue is not None and not prologue.broadcast_operands_only
 
 
 def b_tile_for(tile: TileConfig, src_b: Tensor, K: int, N: int) -> TileConfig:
@@ -151,6 +166,9 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         helpers.append(epi.helper())
         value_expr = epi.scalar_call(["{a0}"], "row", "col")
 
+    if gathers(pro_a) or gathers(pro_b):
+        tile = dataclasses.replace(tile, tile_K=min(tile.tile_K, GATHER_TILE_K))
+        aligned = is_aligned_shape(M, K, N, tile)
     config = MatmulConfig(
         tile=tile,
         aligned=aligned,

@@ -20,12 +20,24 @@ def test_broadcast_only_prologue_is_applied_at_commit():
     assert "ld_B_tile.template fetch<false>(" in src  # no transform on V
 
 
-def test_full_operand_prologue_is_applied_at_fetch():
+def test_full_operand_prologue_gathers_with_the_tile():
     # (h1 * s * h2) @ W3: s and h2 are full matrices, loaded with the A tile
+    # and multiplied in when the chunk is committed; k-chunks of 16
     g = _by_name(compile_program(gpu_cases.mlp_block(128, 128, 384)))["matmul_out_fused"]
-    src = g.kernel.source
-    assert "fetch_raw" not in src.split("extern \"C\"")[1]
-    assert "ld_A_tile.template fetch<false>(" in src and ", xf_A_tile);" in src
+    body = g.kernel.source.split('extern "C"')[1]
+    assert "mt_tile_colvec_g<" in body and ", 2> ld_A_tile;" in body
+    assert "ld_A_tile.template fetch_gather<" in body and "ld_A_tile.template commit_apply<" in body
+    assert "mt_mfma_tile<" in body and ", 16, " in body.split("mt_mfma_tile<")[1].split(">")[0] + ", "
+    assert hip_backend.compile_only(g.kernel.source) > 0
+
+
+def test_gather_switch_off_restores_fetch_time_transform(monkeypatch):
+    from metellus_amd.orchestrator.assembly import matmul as am
+
+    monkeypatch.setattr(am, "GATHER_PROLOGUES", False)
+    g = _by_name(compile_program(gpu_cases.mlp_block(128, 128, 384)))["matmul_out_fused"]
+    body = g.kernel.source.split('extern "C"')[1]
+    assert "fetch_gather" not in body and "ld_A_tile.template fetch<false>(" in body
 
 
 def test_batched_tables_hold_global_pointers_and_compile():
