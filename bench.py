@@ -18,7 +18,7 @@ heads, ``api.run_batch``), each kernel against its roofline.
 ``cpu_baseline``: the CPU oracle (NumPy, single-threaded ufuncs) evaluating
 the same C2 expression on the same full-size inputs for ~10 s on the host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|fragments]
        [--no-extra] [--no-cpu] [--no-flush] [--repeat-kernel NAME --steps K] (profiling)
 """
 
@@ -339,6 +339,99 @@ def cpu_baseline_c2(ops, budget_s: float = 10.0) -> dict:
     }
 
 
+def fragment_benches(steps: int, flusher) -> list[dict]:
+    """The reference's fragment-level benches (tests/bench_init.py,
+    bench_reduction.py, bench_elementwise.py, bench_matmul.py) at their own
+    sizes, composed by hand as in ``tests/fragment_kernels.py``; each launch
+    timed after a cache flush.  Work: bytes read + written once, or 2*M*N*K."""
+    import metellus_amd
+
+    metellus_amd.install_reference_namespace()  # the builders import the reference's module names
+    from metellus_amd.compute.elementwise.elementwise import elementwise_arity
+    from metellus_amd.runtime import hip_backend
+    from metellus_amd.runtime.buffer import Buffer
+    from tests import fragment_kernels as fk
+
+    rng = np.random.default_rng(17)
+    out = []
+
+    def time_one(label, kernel, arrays, out_bytes, dims, grid, threads, work, bound):
+        bufs = [Buffer.from_numpy(a) if isinstance(a, np.ndarray) else Buffer(a) for a in arrays]
+        handle = kernel.handle
+        ms = []
+        for s in range(steps + 2):
+            if flusher is not None:
+                flusher.flush()
+            t = hip_backend.launch(handle, bufs, dims, kernel.dims_slot_index, grid, threads, timed=True)
+            if s >= 2:
+                ms.append(t)
+        for b in bufs:
+            b.release()
+        mean = float(np.mean(ms))
+        if bound == "hbm":
+            achieved, peak, unit = work / (mean * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        else:
+            achieved, peak, unit = work / (mean * 1e-3) / 1e12, FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
+        log(f"[bench] {label}: {mean:.4f} ms  {achieved:.1f} {unit} ({100 * achieved / peak:.1f}%)")
+        out.append({"kernel": kernel.function_name, "config": label, "grid": list(grid), "threads": list(threads),
+                    "ms_mean": round(mean, 5), "ms_min": round(float(np.min(ms)), 5), "bound": bound,
+                    "work": float(work), "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                    "frac": round(achieved / peak, 4)})
+
+    n = 1 << 22  # 4M floats, bench_init's size
+    tg = (fk.TG_X, 1, 1)
+    time_one("bench_init fill 4M", fk.fill_kernel(1.0), [n * 4], 0, (n,), fk.init_grid(n), tg, n * 4, "hbm")
+    time_one("bench_init arange 4M", fk.arange_kernel(0.0, 1.0), [n * 4], 0, (n,), fk.init_grid(n), tg, n * 4, "hbm")
+    src = rng.standard_normal(n).astype(np.float32)
+    time_one("bench_init copy 4M", fk.copy_kernel(), [n * 4, src], 0, (n,), fk.init_grid(n), tg, 2 * n * 4, "hbm")
+
+    m = k = 1024  # bench_reduction's and bench_elementwise's size
+    x = rng.uniform(-1.0, 1.0, (m, k)).astype(np.float32)
+    for op in ("sum", "max", "min", "product"):
+        time_one(f"bench_reduction {op} 1024x1024", fk.reduction_kernel(op), [x, m * 4], 0, (m, k), (m, 1, 1), tg,
+                 x.nbytes + m * 4, "hbm")
+
+    xe = rng.uniform(0.25, 3.75, (m, k)).astype(np.float32)
+    ye = rng.uniform(1.25, 2.25, (m, k)).astype(np.float32)
+    cases = [(op, None, None, "none") for op in ("negate", "exp", "sqrt", "tanh")]
+    cases += [(op, ye, None, "none") for op in ("add", "mul", "div", "max", "lt")]
+    cases += [("add", np.array([[1.5]], np.float32), None, "scalar"),
+              ("add", rng.uniform(0.5, 1.5, (1, k)).astype(np.float32), None, "row"),
+              ("mul", rng.uniform(0.5, 1.5, (m, 1)).astype(np.float32), None, "col"),
+              ("where", ye, (xe > 2.0).astype(np.float32), "none")]
+    for op, y, cond, yb in cases:
+        kernel, bindings, dims, grid, threads = fk.elementwise_kernel(
+            op, m, k, y.shape if y is not None else None, cond.shape if cond is not None else None, yb, "none")
+        arrays = [xe] + ([y] if y is not None else []) + ([cond] if cond is not None else []) + [m * k * 4]
+        work = sum(a.nbytes for a in arrays[:-1]) + m * k * 4
+        assert elementwise_arity(op) == len(arrays) - 1
+        time_one(f"bench_elementwise {op} ({yb}) 1024x1024", kernel, arrays, 0, dims, grid, threads, work, "hbm")
+
+    # the same kernels at a size where bandwidth, not launch latency, decides
+    big = 1 << 26  # 64M floats = 256 MiB
+    time_one("bench_init fill 64M (scale)", fk.fill_kernel(1.0), [big * 4], 0, (big,), fk.init_grid(big), tg,
+             big * 4, "hbm")
+    bsrc = rng.standard_normal(big).astype(np.float32)
+    time_one("bench_init copy 64M (scale)", fk.copy_kernel(), [big * 4, bsrc], 0, (big,), fk.init_grid(big), tg,
+             2 * big * 4, "hbm")
+    del bsrc
+    xb = rng.standard_normal((8192, 8192)).astype(np.float32)
+    time_one("bench_reduction sum 8192x8192 (scale)", fk.reduction_kernel("sum"), [xb, 8192 * 4], 0, (8192, 8192),
+             (8192, 1, 1), tg, xb.nbytes + 8192 * 4, "hbm")
+    kernel, bindings, dims, grid, threads = fk.elementwise_kernel("add", 8192, 8192, (8192, 8192), None, "none", "none")
+    time_one("bench_elementwise add 8192x8192 (scale)", kernel, [xb, xb, 8192 * 8192 * 4], 0, dims, grid, threads,
+             3 * xb.nbytes, "hbm")
+    del xb
+
+    for mm, kk, nn in ((512, 512, 512), (1024, 64, 1024), (4096, 512, 4096), (8192, 64, 8192)):
+        a = rng.standard_normal((mm, kk)).astype(np.float32)
+        b = rng.standard_normal((kk, nn)).astype(np.float32)
+        kernel, tile, aligned, grid = fk.gemm_kernel(mm, kk, nn)
+        time_one(f"bench_matmul {mm}x{kk}x{nn}", kernel, [a, b, mm * nn * 4], 0, (mm, kk, nn), grid,
+                 (tile.tg_x, tile.tg_y, 1), 2.0 * mm * kk * nn, "mfma")
+    return out
+
+
 def read_profile_traffic(name: str) -> float | None:
     """HBM bytes per launch of the C2 kernel from the committed rocprofv3
     PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated)."""
@@ -464,8 +557,11 @@ def main() -> int:
         per_config += time_kernels(prep, args.steps, 2, flush, "copy calibration 64 MiB")
         prep.release()
 
+    if only == "fragments":
+        per_config += fragment_benches(max(3, min(args.steps, 10)), flush)
+
     # ---- other configs -----------------------------------------------------
-    if not args.no_extra and only is None or only not in (None, "c2"):
+    if (not args.no_extra and only is None) or only not in (None, "c2", "fragments"):
         extra_steps = max(3, min(args.steps, 10))
         todo = []
         if only in (None, "c3"):
