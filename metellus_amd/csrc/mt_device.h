@@ -509,6 +509,11 @@ MT_INLINE void mt_mfma_tile(const float* __restrict__ As, const float* __restric
     const unsigned lh = lane >> 5;
     const float* a_base = As + li * LDA + lh * HALF;
     const float* b_base = Bs + (lh * HALF) * LDB + li;
+    // Raise this wave's issue priority while it feeds the matrix core, so a
+    // wave still holding MFMAs is preferred over one writing the next chunk
+    // to LDS or waiting at the barrier (measured +2.6-3.6 % on 4096^3 and
+    // C4 GEMMs).  The priority of instruction issue inside a SIMD only.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s0 = 0; s0 < HALF; s0 += 4) {
         mt_f32x4 a[WM];
@@ -528,6 +533,7 @@ MT_INLINE void mt_mfma_tile(const float* __restrict__ As, const float* __restric
             }
         }
     }
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // Row (within a 32x32 output block) of accumulator register v held by `lane`;
