@@ -106,6 +106,9 @@ def _sum(a: str, b: str) -> str:
     return f"{a} + {b}"
 
 
+FAST_DIVISION = {"div": "mt_div_fast(x, y)", "recip": "mt_div_fast(1.0f, x)"}
+
+
 @dataclass
 class ChainCode:
     """Device helper for ``chain`` with ``seeds`` (names bound to the helper's
@@ -115,6 +118,10 @@ class ChainCode:
     seeds: tuple[str, ...]
     name: str
     externals: list[External] = field(default_factory=list)
+    # Divisions feeding a matmul (operand prologues, register epilogues,
+    # multi-anchor merges) use mt_div_fast: within 1 ulp of the IEEE
+    # quotient, which the matmul bar (1e-4 sqrt(K)) leaves no trace of.
+    fast_div: bool = False
 
     def __post_init__(self) -> None:
         avail = set(self.seeds)
@@ -171,7 +178,10 @@ class ChainCode:
                     subs[ph] = f"(e{self._operand_ext[(i, pos)]})"
                 else:
                     subs[ph] = f"({local[o.name]})"
-            expr = wrap_bool(op.op, substitute(elementwise_expression(op.op), **subs))
+            template = elementwise_expression(op.op)
+            if self.fast_div and op.op in FAST_DIVISION:
+                template = FAST_DIVISION[op.op]
+            expr = wrap_bool(op.op, substitute(template, **subs))
             lines.append(f"    const float v{i} = {expr};")
             cur = f"v{i}"
             local[op.out.name] = cur

@@ -6,6 +6,8 @@
 //
 //   * mt_dims                 dims passed by value in the kernel arguments
 //   * mt_ld4 / mt_st4         128-bit global loads / stores
+//   * mt_div_fast             division feeding a matmul (reciprocal + one
+//                             correction step, IEEE division for edge cases)
 //   * mt_wave_*               wave64 butterfly reductions (fixed order)
 //   * mt_tile_colvec / rowvec / scalar
 //                             cooperative ROWS x COLS tile fetch: global ->
@@ -50,6 +52,27 @@ MT_INLINE mt_f32x4 mt_ld4_nt(const float* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const mt_f32x4*>(p));
 }
 MT_INLINE void mt_st4_nt(float* p, mt_f32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<mt_f32x4*>(p)); }
+
+// x / y where the quotient enters a matmul: hardware reciprocal, the product,
+// and one Newton (Markstein) correction step q + r * (x - q * y) with FMAs --
+// within 1 ulp of the IEEE quotient at a third of the instructions.  Zero,
+// subnormal, huge or non-finite operands and results take the IEEE division.
+MT_INLINE float mt_div_fast(float x, float y) {
+    const float ay = __builtin_fabsf(y);
+    const float r = __builtin_amdgcn_rcpf(y);
+    const float q = x * r;
+    const float v = __builtin_fmaf(__builtin_fmaf(-q, y, x), r, q);
+    const bool ok = ay > 0x1.0p-125f && ay < 0x1.0p+125f && __builtin_fabsf(v) < 0x1.0p+125f;
+    // The IEEE division stays on its (rarely taken) branch: the empty asm
+    // statement emits nothing but cannot be speculated, so the compiler does
+    // not compute the division for every lane and select.
+    if (__builtin_expect(!ok, 0)) {
+        float xs = x;
+        asm volatile("" : "+v"(xs));
+        return xs / y;
+    }
+    return v;
+}
 
 MT_INLINE unsigned mt_lane() { return threadIdx.x & 63u; }
 // Wave index as a scalar (wave-uniform) value.

@@ -80,7 +80,7 @@ def operand_load(
         mode = "rowvec"
     else:
         mode = "scalar"
-    gather = prologue is not None and not prologue.broadcast_operands_only and GATHER_PROLOGUES
+    gather = gathers(prologue)
     lam = prologue.lambda_transform() if prologue is not None and not gather else None
     return TgLoadFragment(
         name=name,
@@ -98,22 +98,32 @@ def operand_load(
         stages=tile.stages,
         mode=mode,
         transform_lambda=lam,
-        defer_transform=prologue is not None and prologue.broadcast_operands_only,
+        defer_transform=prologue is not None and not gather and prologue.broadcast_operands_only,
         gather_lambda=prologue.gather_lambda() if gather else None,
         apply_lambda=prologue.apply_lambda() if gather else None,
         n_gathered=len(prologue.externals) if gather else 0,
     )
 
 
-# Prologues that read full-size operands load them with the tile and apply
-# the chain at commit (gather / apply), on k-chunks of GATHER_TILE_K so the
-# extra registers fit beside a 256x256 tile's accumulators.
+# Prologues load their external operands with the tile and apply the chain
+# when the chunk is committed to LDS (gather / apply), so neither the chunk
+# nor its operands are waited for before the current chunk's MFMAs and the
+# commit issues no loads.  With full-size operands the k-chunks are
+# GATHER_TILE_K wide so the extra registers fit beside a 256x256 tile's
+# accumulators (broadcast operands cost one register per loader slot).
 GATHER_PROLOGUES = True
 GATHER_TILE_K = 16
+# Divisions inside matmul prologues / epilogues / merges use mt_div_fast
+# (reciprocal + one correction step, within 1 ulp of IEEE division).
+FAST_DIV = True
 
 
 def gathers(prologue: ChainCode | None) -> bool:
-    return GATHER_PROLOGUES and prologue is not None and not prologue.broadcast_operands_only
+    return GATHER_PROLOGUES and prologue is not None and len(prologue.externals) > 0
+
+
+def gathers_full_operands(prologue: ChainCode | None) -> bool:
+    return gathers(prologue) and not prologue.broadcast_operands_only
 
 
 def b_tile_for(tile: TileConfig, src_b: Tensor, K: int, N: int) -> TileConfig:
@@ -152,21 +162,21 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
     helpers: list[str] = []
     pro_a = pro_b = None
     if decision.prologue_a:
-        pro_a = ChainCode(decision.prologue_a, (src_a.name,), "prologue_a")
+        pro_a = ChainCode(decision.prologue_a, (src_a.name,), "prologue_a", fast_div=FAST_DIV)
         pro_a.register_extras(extras, base)
         helpers.append(pro_a.helper())
     if decision.prologue_b:
-        pro_b = ChainCode(decision.prologue_b, (src_b.name,), "prologue_b")
+        pro_b = ChainCode(decision.prologue_b, (src_b.name,), "prologue_b", fast_div=FAST_DIV)
         pro_b.register_extras(extras, base)
         helpers.append(pro_b.helper())
     value_expr = None
     if decision.epilogue:
-        epi = ChainCode(decision.epilogue, (anchor.out.name,), "epilogue")
+        epi = ChainCode(decision.epilogue, (anchor.out.name,), "epilogue", fast_div=FAST_DIV)
         epi.register_extras(extras, base)
         helpers.append(epi.helper())
         value_expr = epi.scalar_call(["{a0}"], "row", "col")
 
-    if gathers(pro_a) or gathers(pro_b):
+    if gathers_full_operands(pro_a) or gathers_full_operands(pro_b):
         tile = dataclasses.replace(tile, tile_K=min(tile.tile_K, GATHER_TILE_K))
         aligned = is_aligned_shape(M, K, N, tile)
     config = MatmulConfig(

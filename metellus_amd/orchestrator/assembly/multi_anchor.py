@@ -29,6 +29,7 @@ from metellus_amd.compute.matmul.matmul import (
 from metellus_amd.orchestrator.assembly.decision import DecisionView
 from metellus_amd.orchestrator.assembly.expressions import ChainCode
 from metellus_amd.orchestrator.assembly.extras import Extras, input_param, output_param, param_name
+from metellus_amd.orchestrator.assembly import matmul as _mm
 from metellus_amd.orchestrator.assembly.matmul import b_tile_for, operand_load
 from metellus_amd.orchestrator.ir import Tensor
 from metellus_amd.orchestrator.kernel_group import KernelGroup
@@ -70,14 +71,14 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
     def prologue(chain, src, label):
         if not chain:
             return None
-        code = ChainCode(tuple(chain), (src.name,), label)
+        code = ChainCode(tuple(chain), (src.name,), label, fast_div=_mm.FAST_DIV)
         code.register_extras(extras, base)
         helpers.append(code.helper())
         return code
 
     tf_a = tuple(prologue(pro_a[i], src_a[i], f"prologue_a{i}") for i in range(2))
     tf_b = tuple(prologue(pro_b[i], src_b[i], f"prologue_b{i}") for i in range(2))
-    merge_code = ChainCode((merge,), (a0.out.name, a1.out.name), "merge")
+    merge_code = ChainCode((merge,), (a0.out.name, a1.out.name), "merge", fast_div=_mm.FAST_DIV)
     helpers.append(merge_code.helper())
     value_expr = merge_code.call(["{a0}", "{a1}"], [])
 

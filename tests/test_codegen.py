@@ -11,13 +11,22 @@ def _by_name(groups):
     return {g.kernel.function_name: g for g in groups}
 
 
-def test_broadcast_only_prologue_is_applied_at_commit():
-    # P = e / s1 (a per-row divisor) folded into the P @ V loads
+def test_broadcast_only_prologue_gathers_and_applies_at_commit():
+    # P = e / s1 (a per-row divisor) folded into the P @ V loads: s1 is loaded
+    # with the tile, the (fast) division runs at commit; k-chunks stay 32 wide
     g = _by_name(compile_program(gpu_cases.attention_head(256, 64)))["matmul_O_fused"]
     src = g.kernel.source
-    assert "ld_A_tile.template fetch_raw<false>(" in src
-    assert "ld_A_tile.template commit_xf<" in src
+    assert "mt_tile_colvec_g<" in src and "ld_A_tile.template fetch_gather<false>(" in src
+    assert "ld_A_tile.template commit_apply<" in src
+    assert "mt_div_fast(" in src.split('extern "C"')[0].split("prologue_a")[-1]
     assert "ld_B_tile.template fetch<false>(" in src  # no transform on V
+    assert ", 32, " in src.split("mt_mfma_tile<")[-1].split(">")[0] + ", "
+
+
+def test_elementwise_division_stays_ieee():
+    g = compile_program(gpu_cases.softmax(32, 100))[-1]  # p = e / s1 as an elementwise kernel
+    assert "mt_div_fast(" not in g.kernel.source.split('extern "C"')[1]
+    assert "mt_div_fast(" not in "".join(g.kernel.ctx.helpers)
 
 
 def test_full_operand_prologue_gathers_with_the_tile():

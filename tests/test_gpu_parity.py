@@ -196,9 +196,10 @@ def test_register_epilogue_and_prologue():
 
 
 @pytest.mark.parametrize("layout", ["rowmajor", "transposed", "transposed_odd"])
-def test_broadcast_prologues_applied_at_commit(layout):
-    """Prologues reading only broadcast operands are applied when the tile is
-    written to LDS (fetch_raw / commit_xf).  A is loaded 128-bit along
+def test_broadcast_prologues_gathered(layout):
+    """Prologues reading only broadcast operands load those operands with the
+    tile (fetch_gather) and are applied when the tile is written to LDS
+    (commit_apply), with 32-wide k-chunks.  A is loaded 128-bit along
     columns (row-major), 128-bit along rows (transposed view, column stride
     100) or element by element (transposed view, column stride 101); B
     (N = 90) by elements.  M, N are not tile multiples, so bounds apply."""
@@ -226,7 +227,8 @@ def test_broadcast_prologues_applied_at_commit(layout):
     assert [g.strategy for g in res.groups] == [FusionStrategy.ELEMENTWISE_PROLOGUE_MATMUL]
     src = res.groups[0].kernel.source
     # A and B loaders, each once before the k loop and once inside it
-    assert src.count("fetch_raw<true>") == 4 and src.count("commit_xf<") == 4
+    assert src.count("fetch_gather<true>") == 4 and src.count("commit_apply<") == 4
+    assert "fetch_raw<" not in src.split('extern "C"')[1]
     ref = evaluate(ops)
     _check_matmul(res.env["C"], ref["a2"], ref["b1"], ref["C"])
 
