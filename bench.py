@@ -8,7 +8,9 @@ A *step* is one launch of the workload's fused kernel(s) on inputs already
 resident in HBM.  Before every timed step the 256 MiB Infinity Cache is
 flushed by reading a 512 MiB scratch buffer (outside the event bracket), so
 the bandwidth is HBM bandwidth.  Kernel durations come from HIP events
-recorded on the shim's stream around each launch.
+recorded on the shim's stream around each launch.  Each kernel is first run
+(flush, launch) for at least 50 ms of its own GPU time, so the clocks have
+settled before the timed launches.
 
 Also measured (``per_kernel``): C3 softmax (4 kernels), the 4096^3 matmul,
 C4 MLP block (literal 4-kernel partition and the fused diamond variant), C5
@@ -19,7 +21,7 @@ heads, ``api.run_batch``), each kernel against its roofline.
 the same C2 expression on the same full-size inputs for ~10 s on the host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|fragments]
-       [--no-extra] [--no-cpu] [--no-flush] [--repeat-kernel NAME --steps K] (profiling)
+       [--no-extra] [--no-cpu] [--no-flush] [--calibrate-copy]
 """
 
 from __future__ import annotations
@@ -241,13 +243,35 @@ class Flusher:
         self.dst.release()
 
 
+# Warm-up before a kernel's timed launches: at least WARM_MS of its own GPU
+# time, run the way the timed launches are (flush, launch).  Measured on
+# MI355X: the fp32 MFMA kernels start ~20 % slower (the clocks are still
+# rising) and settle after ~15 ms of sustained work; with a 2-launch warm-up
+# the attention S kernel read 351-374 us on its first launches and 293 us
+# settled.  HBM-bound kernels run at their settled rate from the first launch.
+WARM_MS = 50.0
+WARM_MAX_LAUNCHES = 400
+
+
+def warm_up(launch, flusher, min_launches: int = 2) -> int:
+    """Flush + launch until ``WARM_MS`` of kernel time have run (and at
+    least ``min_launches`` launches); returns the number of launches."""
+    total, n = 0.0, 0
+    while n < min_launches or (total < WARM_MS and n < WARM_MAX_LAUNCHES):
+        if flusher is not None:
+            flusher.flush()
+        total += launch(True)
+        n += 1
+    return n
+
+
 def time_kernels(prep: Prepared, steps: int, warmup: int, flusher, label: str) -> list[dict]:
-    """Per kernel: warm up, then ``steps`` event-timed launches, each after
-    an Infinity Cache flush (when ``flusher`` is given)."""
+    """Per kernel: warm up (``warm_up``), then ``steps`` event-timed
+    launches, each after an Infinity Cache flush (when ``flusher`` is
+    given)."""
     out = []
     for i, g in enumerate(prep.groups):
-        for _ in range(warmup):
-            prep.launch(i)
+        warm_up(lambda timed, i=i: prep.launch(i, timed=timed), flusher, warmup)
         prep.hip.synchronize()
         ms = []
         for s in range(steps):
@@ -281,7 +305,8 @@ def time_kernels(prep: Prepared, steps: int, warmup: int, flusher, label: str) -
                 "frac": round(achieved / peak, 4),
             }
         )
-        log(f"[bench] {label} {g.kernel.function_name}: {mean:.4f} ms  {achieved:.1f} {unit} ({100*achieved/peak:.1f}%)")
+        log(f"[bench] {label} {g.kernel.function_name}: {mean:.4f} ms (median {np.median(ms):.4f})  "
+            f"{achieved:.1f} {unit} ({100*achieved/peak:.1f}%)")
     return out
 
 
@@ -358,13 +383,16 @@ def fragment_benches(steps: int, flusher) -> list[dict]:
     def time_one(label, kernel, arrays, out_bytes, dims, grid, threads, work, bound):
         bufs = [Buffer.from_numpy(a) if isinstance(a, np.ndarray) else Buffer(a) for a in arrays]
         handle = kernel.handle
+
+        def launch(timed):
+            return hip_backend.launch(handle, bufs, dims, kernel.dims_slot_index, grid, threads, timed=timed)
+
+        warm_up(launch, flusher)
         ms = []
-        for s in range(steps + 2):
+        for s in range(steps):
             if flusher is not None:
                 flusher.flush()
-            t = hip_backend.launch(handle, bufs, dims, kernel.dims_slot_index, grid, threads, timed=True)
-            if s >= 2:
-                ms.append(t)
+            ms.append(launch(True))
         for b in bufs:
             b.release()
         mean = float(np.mean(ms))
@@ -487,8 +515,7 @@ def main() -> int:
         log("[bench] C2 sigmoid chain 4096x4096: preparing")
         prep = time_prep = Prepared(_c2())
         assert len(prep.groups) == 1
-        for _ in range(args.warmup):
-            prep.launch(0)
+        warm_up(lambda timed: prep.launch(0, timed=timed), flush, args.warmup)
         hip_backend.synchronize()
         kernel_ms = []
         t0 = time.perf_counter()
@@ -562,7 +589,7 @@ def main() -> int:
 
     # ---- other configs -----------------------------------------------------
     if (not args.no_extra and only is None) or only not in (None, "c2", "fragments"):
-        extra_steps = max(3, min(args.steps, 10))
+        extra_steps = max(3, args.steps)
         todo = []
         if only in (None, "c3"):
             todo.append(("C3 softmax 8192x8192", _c3))
