@@ -119,7 +119,7 @@ class ChainCode:
     name: str
     externals: list[External] = field(default_factory=list)
     # Divisions feeding a matmul (operand prologues, register epilogues,
-    # multi-anchor merges) use mt_div_fast: within 1 ulp of the IEEE
+    # multi-anchor merges) use mt_div_fast: within 2 ulp of the IEEE
     # quotient, which the matmul bar (1e-4 sqrt(K)) leaves no trace of.
     fast_div: bool = False
 
@@ -153,6 +153,18 @@ class ChainCode:
         broadcast (small, cache-resident reads)."""
         small = (BroadcastSpec.ROW, BroadcastSpec.COL, BroadcastSpec.SCALAR)
         return all(e.broadcast in small for e in self.externals)
+
+    def external_axes(self) -> frozenset[str]:
+        """Output coordinates (``"row"``, ``"col"``) the external operands'
+        values depend on -- read off the same offsets the gathers emit."""
+        axes = set()
+        for e in self.externals:
+            off = e.offset("mt_r_", "mt_c_")
+            if "mt_r_" in off:
+                axes.add("row")
+            if "mt_c_" in off:
+                axes.add("col")
+        return frozenset(axes)
 
     @property
     def arity(self) -> int:

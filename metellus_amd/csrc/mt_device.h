@@ -6,8 +6,8 @@
 //
 //   * mt_dims                 dims passed by value in the kernel arguments
 //   * mt_ld4 / mt_st4         128-bit global loads / stores
-//   * mt_div_fast             division feeding a matmul (reciprocal + one
-//                             correction step, IEEE division for edge cases)
+//   * mt_div_fast             division feeding a matmul (refined reciprocal
+//                             times x, within 2 ulp; IEEE division at the edges)
 //   * mt_wave_*               wave64 butterfly reductions (fixed order)
 //   * mt_tile_colvec / rowvec / scalar
 //                             cooperative ROWS x COLS tile fetch: global ->
@@ -53,16 +53,27 @@ MT_INLINE mt_f32x4 mt_ld4_nt(const float* p) {
 }
 MT_INLINE void mt_st4_nt(float* p, mt_f32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<mt_f32x4*>(p)); }
 
-// x / y where the quotient enters a matmul: hardware reciprocal, the product,
-// and one Newton (Markstein) correction step q + r * (x - q * y) with FMAs --
-// within 1 ulp of the IEEE quotient at a third of the instructions.  Zero,
-// subnormal, huge or non-finite operands and results take the IEEE division.
+// x / y where the quotient enters a matmul.  r is the hardware reciprocal
+// refined by one Newton step, r + r * (1 - y * r); it depends on y only, so
+// the compiler computes it once per distinct divisor (a row or column
+// broadcast operand gives one per loaded vector), and each element costs:
+//   * 1 <= |y| < 2^125: the product x * r -- within 2 ulp of the IEEE
+//     quotient; |x * r| <= |x|, so nothing overflows, and zero, infinite
+//     and NaN numerators give what the division gives;
+//   * 2^-125 < |y| < 1: the product plus one residual (Markstein) correction
+//     q + r * (x - q * y) -- within 1 ulp;
+//   * anything else (zero, subnormal, huge or non-finite divisors, quotients
+//     of 2^125 and beyond on the second path): the IEEE division.
+// Measured on the C5 P.V kernel (one division per A element): 296 us with
+// the correction on every element, 276 us with the product alone.
 MT_INLINE float mt_div_fast(float x, float y) {
     const float ay = __builtin_fabsf(y);
-    const float r = __builtin_amdgcn_rcpf(y);
+    float r = __builtin_amdgcn_rcpf(y);
+    r = __builtin_fmaf(__builtin_fmaf(-y, r, 1.0f), r, r);
     const float q = x * r;
+    if (__builtin_expect(ay >= 1.0f && ay < 0x1.0p+125f, 1)) return q;
     const float v = __builtin_fmaf(__builtin_fmaf(-q, y, x), r, q);
-    const bool ok = ay > 0x1.0p-125f && ay < 0x1.0p+125f && __builtin_fabsf(v) < 0x1.0p+125f;
+    const bool ok = ay > 0x1.0p-125f && ay < 1.0f && __builtin_fabsf(v) < 0x1.0p+125f;
     // The IEEE division stays on its (rarely taken) branch: the empty asm
     // statement emits nothing but cannot be speculated, so the compiler does
     // not compute the division for every lane and select.
@@ -369,7 +380,12 @@ struct mt_tile_scalar {
 // element) and applies the chain when the tile is committed to LDS
 // (commit_apply: a(raw, extras) per in-bounds element), so neither the tile
 // nor its operands are waited for before the current chunk's MFMAs.  Out of
-// bounds elements stay 0 and are not transformed.
+// bounds elements stay 0 and are not transformed.  SLOT = true (vectorised
+// loaders): the operands are constant along the vector axis (a column
+// broadcast for mt_tile_colvec_g, a row broadcast for mt_tile_rowvec_g), so
+// they are gathered once per 128-bit slot and the 4 elements share them --
+// one value, so work that depends only on it (a divisor's reciprocal) is
+// done once per slot.
 // ---------------------------------------------------------------------------
 
 template <int E>
@@ -377,13 +393,14 @@ struct mt_vals {
     float v[E];
 };
 
-template <int ROWS, int COLS, int NT, int E>
+template <int ROWS, int COLS, int NT, int E, bool SLOT = false>
 struct mt_tile_colvec_g : mt_tile_colvec<ROWS, COLS, NT> {
     using Base = mt_tile_colvec<ROWS, COLS, NT>;
     using Base::CV;
     using Base::PER;
     using Base::TOTAL;
-    mt_vals<E> ex[PER][4];
+    static constexpr int NG = SLOT ? 1 : 4;  // gathers per slot
+    mt_vals<E> ex[PER][NG];
 
     template <bool CHECK, typename G>
     MT_INLINE void fetch_gather(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
@@ -398,7 +415,7 @@ struct mt_tile_colvec_g : mt_tile_colvec<ROWS, COLS, NT> {
             if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rlim && gc < clim))) {
                 x = mt_ld4(src + (size_t)gr * rs + gc);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) ex[i][j] = g(gr, gc + (unsigned)j);
+                for (int j = 0; j < NG; ++j) ex[i][j] = g(gr, gc + (unsigned)j);
             }
             this->v[i] = x;
         }
@@ -413,22 +430,23 @@ struct mt_tile_colvec_g : mt_tile_colvec<ROWS, COLS, NT> {
             const unsigned gr = this->r0 + r, gc = this->c0 + c;
             if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < this->rl && gc < this->cl))) {
                 this->v[i].x = a(this->v[i].x, ex[i][0]);
-                this->v[i].y = a(this->v[i].y, ex[i][1]);
-                this->v[i].z = a(this->v[i].z, ex[i][2]);
-                this->v[i].w = a(this->v[i].w, ex[i][3]);
+                this->v[i].y = a(this->v[i].y, ex[i][1 % NG]);
+                this->v[i].z = a(this->v[i].z, ex[i][2 % NG]);
+                this->v[i].w = a(this->v[i].w, ex[i][3 % NG]);
             }
         }
         Base::template commit<LD>(lds, tid);
     }
 };
 
-template <int ROWS, int COLS, int NT, int E>
+template <int ROWS, int COLS, int NT, int E, bool SLOT = false>
 struct mt_tile_rowvec_g : mt_tile_rowvec<ROWS, COLS, NT> {
     using Base = mt_tile_rowvec<ROWS, COLS, NT>;
     using Base::RV;
     using Base::PER;
     using Base::TOTAL;
-    mt_vals<E> ex[PER][4];
+    static constexpr int NG = SLOT ? 1 : 4;  // gathers per slot
+    mt_vals<E> ex[PER][NG];
 
     template <bool CHECK, typename G>
     MT_INLINE void fetch_gather(const float* __restrict__ src, unsigned cs, unsigned row0, unsigned col0,
@@ -443,7 +461,7 @@ struct mt_tile_rowvec_g : mt_tile_rowvec<ROWS, COLS, NT> {
             if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < rlim && gc < clim))) {
                 x = mt_ld4(src + gr + (size_t)gc * cs);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) ex[i][j] = g(gr + (unsigned)j, gc);
+                for (int j = 0; j < NG; ++j) ex[i][j] = g(gr + (unsigned)j, gc);
             }
             this->v[i] = x;
         }
@@ -458,9 +476,9 @@ struct mt_tile_rowvec_g : mt_tile_rowvec<ROWS, COLS, NT> {
             const unsigned gr = this->r0 + r, gc = this->c0 + c;
             if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < this->rl && gc < this->cl))) {
                 this->v[i].x = a(this->v[i].x, ex[i][0]);
-                this->v[i].y = a(this->v[i].y, ex[i][1]);
-                this->v[i].z = a(this->v[i].z, ex[i][2]);
-                this->v[i].w = a(this->v[i].w, ex[i][3]);
+                this->v[i].y = a(this->v[i].y, ex[i][1 % NG]);
+                this->v[i].z = a(this->v[i].z, ex[i][2 % NG]);
+                this->v[i].w = a(this->v[i].w, ex[i][3 % NG]);
             }
         }
         Base::template commit<LD>(lds, tid);

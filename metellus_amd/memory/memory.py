@@ -92,6 +92,10 @@ class TgLoadFragment:
     gather_lambda: str | None = None
     apply_lambda: str | None = None
     n_gathered: int = 0
+    # The gathered operands are constant along the loader's vector axis (a
+    # column broadcast for "colvec", a row broadcast for "rowvec"): gather
+    # them once per 128-bit slot.
+    gather_per_slot: bool = False
 
     @property
     def pitch(self) -> str:
@@ -146,8 +150,11 @@ class TgLoadFragment:
         if self.gathering:
             if mode == "colvec_safe" or self.apply_lambda is None or self.n_gathered < 1:
                 raise ValueError(f"{self.name}: gather/apply needs a proven load mode and an apply lambda")
+            if self.gather_per_slot and mode not in ("colvec", "rowvec"):
+                raise ValueError(f"{self.name}: per-slot gathers need a vectorised load mode")
+            slot = ", true" if self.gather_per_slot else ""
             return (
-                f"{tmpl}_g<{rows}, {cols}, {self.num_threads}, {self.n_gathered}> {self.loader};\n"
+                f"{tmpl}_g<{rows}, {cols}, {self.num_threads}, {self.n_gathered}{slot}> {self.loader};\n"
                 f"const auto xg_{self.dst_name} = {self.gather_lambda};\n"
                 f"const auto xa_{self.dst_name} = {self.apply_lambda};"
             )

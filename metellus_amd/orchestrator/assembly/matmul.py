@@ -82,6 +82,9 @@ def operand_load(
         mode = "scalar"
     gather = gathers(prologue)
     lam = prologue.lambda_transform() if prologue is not None and not gather else None
+    # one gather per 128-bit slot when the operands do not change along it
+    along = {"colvec": "col", "rowvec": "row"}.get(mode)
+    per_slot = gather and along is not None and along not in prologue.external_axes()
     return TgLoadFragment(
         name=name,
         src_name=param_name(src.buffer_key),
@@ -102,6 +105,7 @@ def operand_load(
         gather_lambda=prologue.gather_lambda() if gather else None,
         apply_lambda=prologue.apply_lambda() if gather else None,
         n_gathered=len(prologue.externals) if gather else 0,
+        gather_per_slot=per_slot,
     )
 
 
@@ -114,7 +118,7 @@ def operand_load(
 GATHER_PROLOGUES = True
 GATHER_TILE_K = 16
 # Divisions inside matmul prologues / epilogues / merges use mt_div_fast
-# (reciprocal + one correction step, within 1 ulp of IEEE division).
+# (a refined reciprocal times the numerator, within 2 ulp of IEEE division).
 FAST_DIV = True
 
 

@@ -1,7 +1,10 @@
 """``mt_div_fast`` (division where the quotient enters a matmul) against
-IEEE division on the GPU: within 1 ulp for every finite pair, identical
-(NaN matching NaN) where an operand or the result is zero, subnormal, huge,
-infinite or NaN (those take the IEEE path)."""
+IEEE division on the GPU.  Divisors with 1 <= |y| < 2^125 take the
+refined-reciprocal product: within 2 ulp, and identical for zero, infinite
+and NaN numerators.  Divisors with 2^-125 < |y| < 1 add one residual
+correction: within 1 ulp.  Zero, subnormal, huge and non-finite divisors
+(and huge quotients of small divisors) take the IEEE path: identical, NaN
+matching NaN."""
 
 import numpy as np
 import pytest
@@ -50,15 +53,25 @@ def test_fast_division_matches_ieee():
     for b in (bx, by, bf, bi):
         b.release()
     np.testing.assert_array_equal(ieee, x / y)  # the device division is IEEE
-    edge = ~(np.isfinite(x) & np.isfinite(y) & np.isfinite(ieee)) | (np.abs(y) < 2.0 ** -125) \
-        | (np.abs(y) > 2.0 ** 125) | (np.abs(ieee) > 2.0 ** 124)
-    np.testing.assert_array_equal(fast[edge], ieee[edge])
-    normal = ~edge & (np.abs(ieee) > 2.0 ** -126)  # quotients in the normal range
-    d = _ulp_distance(fast[normal], ieee[normal])
-    assert d.max() <= 1, f"max ulp distance {d.max()}"
-    exact = float(np.mean(d == 0))
-    print(f"mt_div_fast: {exact:.6%} of {normal.sum()} normal quotients exact, max 1 ulp")
-    assert exact > 0.99
-    # subnormal quotients: within float32 absolute resolution there
-    sub = ~edge & ~normal
+    ay = np.abs(y)
+    ieee_path = ~np.isfinite(y) | (ay <= 2.0 ** -125) | (ay >= 2.0 ** 125) | ~np.isfinite(x) \
+        | ((ay < 1.0) & (np.abs(ieee) > 2.0 ** 126))
+    np.testing.assert_array_equal(fast[ieee_path], ieee[ieee_path])
+    finite = ~ieee_path & np.isfinite(ieee)
+    product = finite & (ay >= 1.0)
+    corrected = finite & (ay < 1.0)
+    normal = np.abs(ieee) > 2.0 ** -126  # quotients in the normal range
+    d_prod = _ulp_distance(fast[product & normal], ieee[product & normal])
+    d_corr = _ulp_distance(fast[corrected & normal], ieee[corrected & normal])
+    assert d_prod.max() <= 2, f"product path: max ulp distance {d_prod.max()}"
+    assert d_corr.max() <= 1, f"corrected path: max ulp distance {d_corr.max()}"
+    exact_prod, exact_corr = float(np.mean(d_prod == 0)), float(np.mean(d_corr == 0))
+    print(f"mt_div_fast: product path {exact_prod:.4%} exact of {d_prod.size} (max {d_prod.max()} ulp); "
+          f"corrected path {exact_corr:.4%} exact of {d_corr.size}")
+    assert exact_prod > 0.6 and exact_corr > 0.99
+    # zero numerators keep their sign on the product path; subnormal
+    # quotients stay within float32's absolute resolution there
+    zero = product & (x == 0)
+    np.testing.assert_array_equal(fast[zero].view(np.uint32), ieee[zero].view(np.uint32))
+    sub = finite & ~normal
     assert np.all(np.abs(fast[sub].astype(np.float64) - ieee[sub]) <= 2.0 ** -148)
