@@ -132,7 +132,7 @@ class Prepared:
         g = self.groups[i]
         return self.hip.launch(
             g.kernel.handle, [self.env[k] for k in g.bindings], g.dims, g.kernel.dims_slot_index,
-            g.grid, g.threads, timed=timed,
+            g.grid, g.threads, timed=timed, workspace=g.kernel.workspace_bytes,
         )
 
     def run_all(self):
@@ -278,6 +278,7 @@ def time_kernels(prep: Prepared, steps: int, warmup: int, flusher, label: str) -
             if flusher is not None:
                 flusher.flush()
             ms.append(prep.launch(i, timed=True))
+        prep.hip.check_workspace()  # raises if a stream-K launch gave up waiting
         bound, work = kernel_work(g, prep.owner)
         work *= getattr(prep, "B", 1)
         mean = float(np.mean(ms))

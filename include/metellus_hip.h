@@ -105,6 +105,22 @@ int mt_sync(void);
  * served from a cache (hits); for tests of the cache. */
 int mt_cache_stats(uint64_t* compiled, uint64_t* hits);
 
+/* No counterpart in the reference, whose matmul dispatches are one tile per
+ * threadgroup (reference: src/compute/matmul/config.py:36-37).  Handle of
+ * the shim's device workspace, at least nbytes (>= 4096): a stream-K
+ * matmul kernel takes it as its last parameter, after the dims.  Its first
+ * 4096 bytes are flag words, zero when created and left zero by every
+ * launch that completes; growing it frees the old one in stream order.  The
+ * handle belongs to the shim (mt_free refuses it).  Launches that share the
+ * workspace are ordered by the shim's single stream. */
+int mt_workspace(size_t nbytes, uint64_t* handle);
+
+/* Read (synchronously) and clear the workspace's error word: nonzero when a
+ * stream-K workgroup gave up waiting for a partial tile, in which case the
+ * results of that launch are invalid and the flag words are reset to 0.
+ * *error = 0 when no workspace exists. */
+int mt_workspace_check(uint32_t* error);
+
 #ifdef __cplusplus
 }
 #endif

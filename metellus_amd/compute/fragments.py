@@ -19,7 +19,9 @@ Rendered kernel layout::
 Dims travel in the kernel-argument segment as a fixed 16-word struct
 (``mt_dims``) at ``dims_buffer_index`` (default: after the buffers), instead of
 the per-launch dims buffer the reference allocates (reference:
-src/runtime/program.py:186).
+src/runtime/program.py:186).  A kernel with ``workspace_bytes`` (stream-K
+matmuls) takes one more parameter, ``float* mt_ws``, after everything else;
+the runtime passes the shim's workspace there.
 """
 
 from __future__ import annotations
@@ -63,6 +65,9 @@ class CodegenContext:
     dims_buffer_index: int | None = None
     tg_z: int = 1
     batched: bool = False
+    # Bytes of device workspace the kernel takes as its last parameter
+    # (``float* mt_ws``, after the dims); 0 = none.
+    workspace_bytes: int = 0
 
     @property
     def num_threads(self) -> int:
@@ -173,6 +178,10 @@ class CodegenEngine:
         else:
             params, picks = list(ctx.buffers), []
         params.insert(dims_index, "const mt_dims dims")
+        if ctx.workspace_bytes:
+            if ctx.batched:
+                raise ValueError(f"{ctx.function_name}: a kernel with a workspace is not batched")
+            params.append("float* mt_ws")
         body_parts = [
             *picks,
             self._dim_decls(ctx.dims),

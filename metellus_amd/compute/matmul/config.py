@@ -165,6 +165,12 @@ def tile_score(t: TileConfig, M: int, N: int, anchors: int = 1, batch: int = 1) 
 
 PERSISTENT = True  # tuning switch for the persistent tile loop
 PERSISTENT_CAPACITY: int | None = None  # override of resident workgroups (tests)
+# Split the last partial round of a persistent loop by k-chunks (stream-K)
+# instead of leaving workgroups idle; single (unbatched) problems only, and
+# at most STREAM_K_MAX_WORKGROUPS workgroups (the workspace head holds one
+# flag word per workgroup and the error word: MT_WS_HEAD - 1 flags).
+STREAM_K = True
+STREAM_K_MAX_WORKGROUPS = 1023
 
 
 def resident_workgroups(t: TileConfig, anchors: int = 1) -> int:
@@ -185,6 +191,18 @@ def persistent_workgroups(M: int, N: int, t: TileConfig, batch: int = 1) -> int 
     if tiles * batch <= capacity:
         return None
     return min(tiles, max(1, capacity // batch))
+
+
+def uses_stream_k(M: int, K: int, N: int, t: TileConfig, workgroups: int | None, batch: int = 1) -> bool:
+    """A persistent loop of ``workgroups`` whose tiles are not a whole
+    number of rounds: the last round runs as stream-K -- when its k-chunks
+    are at least as many as the workgroups, so every workgroup's range holds
+    work and a split tile's contributors are the workgroups just below its
+    owner (the kernel's fixup relies on that)."""
+    if not STREAM_K or workgroups is None or batch != 1 or workgroups > STREAM_K_MAX_WORKGROUPS:
+        return False
+    rem = (ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N)) % workgroups
+    return rem != 0 and rem * ceil_div(K, t.tile_K) >= workgroups
 
 
 def select_tile_config(M: int, K: int, N: int, anchors: int = 1, batch: int = 1) -> TileConfig:

@@ -53,20 +53,39 @@ class PersistentTiles:
     outnumber the workgroups the GPU holds at once: the next tile's first
     k-chunk is then loaded during the current tile's last one, and the
     current tile's stores drain while the next tile's MFMAs run, instead of
-    each workgroup paying its own launch, first load and store phases."""
+    each workgroup paying its own launch, first load and store phases.
+
+    ``stream_k``: when the tiles are not a multiple of P, the last partial
+    round is split by k-chunks instead of by tiles (``mt_stream_k`` in the
+    device library): every workgroup gets the same number of chunks, and
+    tiles split between workgroups are summed through the workspace
+    (``StreamKFixupFragment``).  Each loop item is a tile and a chunk range
+    ``[mt_kb, mt_ke)``; in the plain loop every item is a whole tile."""
 
     tile_M: int
     tile_N: int
     M_dim_var: str = "M"
     N_dim_var: str = "N"
+    stream_k: bool = False
+    tile_K: int = 32
+    K_dim_var: str = "K"
+
+
+def stream_k_workspace_bytes(tile_M: int, tile_N: int, workgroups: int, anchors: int = 1) -> int:
+    """Workspace of a stream-K kernel: the flag words, then one partial tile
+    (every accumulator set) per workgroup."""
+    return 4 * (STREAM_K_HEAD_WORDS + workgroups * tile_M * tile_N * anchors)
+
+
+STREAM_K_HEAD_WORDS = 1024  # MT_WS_HEAD in the device library
 
 
 @dataclass(frozen=True)
 class MatmulTileMappingFragment:
     """``tg`` = (column tile, row tile) of this workgroup; with ``persistent``
     it opens the tile loop (closed by ``PersistentLoopEndFragment``) and
-    defines ``mt_first_tile``, ``mt_has_next``, ``mt_next_m0/n0`` for the
-    mainloop's cross-tile prefetch."""
+    defines ``mt_first_tile``, ``mt_has_next``, ``mt_next_m0/n0/kb`` and the
+    item's chunk range ``mt_kb``/``mt_ke`` for the mainloop."""
 
     persistent: PersistentTiles | None = None
     name: str = "tile_mapping"
@@ -76,18 +95,127 @@ class MatmulTileMappingFragment:
         p = self.persistent
         if p is None:
             return "const uint3 tg = make_uint3(blockIdx.x, blockIdx.y, blockIdx.z);"
+        head = [
+            f"const unsigned mt_tiles_x = ({p.N_dim_var} + {p.tile_N - 1}u) / {p.tile_N}u;",
+            f"const unsigned mt_tiles = mt_tiles_x * (({p.M_dim_var} + {p.tile_M - 1}u) / {p.tile_M}u);",
+            "unsigned mt_stage = 0u;  // LDS buffer holding the current k-chunk",
+        ]
+        if p.stream_k:
+            if ctx.batched:
+                raise ValueError("stream-K matmuls are not batched")
+            return "\n".join(
+                [
+                    *head,
+                    f"const unsigned mt_chunks = ({p.K_dim_var} + {p.tile_K - 1}u) / {p.tile_K}u;",
+                    "mt_stream_k mt_sk;",
+                    "mt_sk.init(mt_tiles, mt_chunks, gridDim.x, blockIdx.x);",
+                    "for (unsigned mt_item = 0u; mt_item < mt_sk.items(); ++mt_item) {",
+                    "const bool mt_first_tile = mt_item == 0u;",
+                    "unsigned mt_t, mt_kb, mt_ke;",
+                    "mt_sk.item(mt_item, mt_t, mt_kb, mt_ke);",
+                    "const bool mt_has_next = mt_item + 1u < mt_sk.items();",
+                    "unsigned mt_t_next = 0u, mt_next_kb = 0u, mt_next_ke = 0u;",
+                    "if (mt_has_next) mt_sk.item(mt_item + 1u, mt_t_next, mt_next_kb, mt_next_ke);",
+                    f"const unsigned mt_next_m0 = (mt_t_next / mt_tiles_x) * {p.tile_M}u;",
+                    f"const unsigned mt_next_n0 = (mt_t_next % mt_tiles_x) * {p.tile_N}u;",
+                    "const uint3 tg = make_uint3(mt_t % mt_tiles_x, mt_t / mt_tiles_x, blockIdx.z);",
+                ]
+            )
         return "\n".join(
             [
-                f"const unsigned mt_tiles_x = ({p.N_dim_var} + {p.tile_N - 1}u) / {p.tile_N}u;",
-                f"const unsigned mt_tiles = mt_tiles_x * (({p.M_dim_var} + {p.tile_M - 1}u) / {p.tile_M}u);",
-                "unsigned mt_stage = 0u;  // LDS buffer holding the current k-chunk",
+                *head,
                 "for (unsigned mt_t = blockIdx.x; mt_t < mt_tiles; mt_t += gridDim.x) {",
                 "const bool mt_first_tile = mt_t == blockIdx.x;",
                 "const unsigned mt_t_next = mt_t + gridDim.x;",
                 "const bool mt_has_next = mt_t_next < mt_tiles;",
                 f"const unsigned mt_next_m0 = (mt_t_next / mt_tiles_x) * {p.tile_M}u;",
                 f"const unsigned mt_next_n0 = (mt_t_next % mt_tiles_x) * {p.tile_N}u;",
+                "const unsigned mt_kb = 0u, mt_next_kb = 0u;",
+                f"const unsigned mt_ke = ({p.K_dim_var} + {p.tile_K - 1}u) / {p.tile_K}u;",
                 "const uint3 tg = make_uint3(mt_t % mt_tiles_x, mt_t / mt_tiles_x, blockIdx.z);",
+            ]
+        )
+
+    @property
+    def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
+        return ()
+
+
+@dataclass(frozen=True)
+class StreamKFixupFragment:
+    """Between a stream-K item's mainloop and its epilogue.  A contributor
+    (its chunk range starts inside the tile) stores its accumulators to its
+    workspace slot -- registers 4q..4q+3 of block b of lane t as one float4
+    at index ``(4b + q) * NT + t``, so every store and load is one coalesced
+    1 KiB row per wave -- raises its flag and
+    moves on to its next item.  An owner whose range ends inside the tile
+    waits for the following ranges (workgroups w-1, w-2, ...), adds their
+    partials in that order, then runs the epilogue as for a whole tile."""
+
+    config: MatmulConfig
+    suffixes: tuple[str, ...] = ("",)
+    name: str = "stream_k_fixup"
+    kind: str = "store"
+
+    def render(self, ctx: CodegenContext) -> str:
+        t = self.config.tile
+        nt = t.num_threads
+        blocks = t.WM * t.WN
+        tile_floats = t.tile_M * t.tile_N * len(self.suffixes)
+        stores, adds = [], []
+        for k, sfx in enumerate(self.suffixes):
+            # quad q of block b (registers 4q..4q+3) of lane t at float4 index (b * 4 + q) * NT + t
+            base = k * blocks
+            loop = [
+                "#pragma unroll",
+                f"for (int i = 0; i < {t.WM}; ++i)",
+                "#pragma unroll",
+                f"    for (int j = 0; j < {t.WN}; ++j) {{",
+                f"        const size_t mt_q0 = (size_t)({base}u + (unsigned)(i * {t.WN} + j)) * {4 * nt}u + threadIdx.x;",
+                "#pragma unroll",
+                "        for (int q = 0; q < 4; ++q) {",
+            ]
+            quad = f"acc{sfx}[i][j][4 * q], acc{sfx}[i][j][4 * q + 1], acc{sfx}[i][j][4 * q + 2], acc{sfx}[i][j][4 * q + 3]"
+            stores += [
+                *loop,
+                f"            mt_part4[mt_q0 + (size_t)q * {nt}u] = mt_f32x4{{{quad}}};",
+                "        }",
+                "    }",
+            ]
+            # Per quad, a short loop over the contributors carries only that
+            # quad, so the fixup's register use stays near the mainloop's and
+            # nothing the mainloop keeps live is spilled for it.
+            adds += [
+                *loop,
+                f"            mt_f32x4 mt_s = mt_f32x4{{{quad}}};",
+                "            for (unsigned mt_c = 1u; mt_c <= mt_nc; ++mt_c)",
+                f"                mt_s += reinterpret_cast<const mt_f32x4*>(mt_ws_part(mt_ws, blockIdx.x - mt_c, {tile_floats}u))"
+                f"[mt_q0 + (size_t)q * {nt}u];",
+                "#pragma unroll",
+                f"            for (int e = 0; e < 4; ++e) acc{sfx}[i][j][4 * q + e] = mt_s[e];",
+                "        }",
+                "    }",
+            ]
+        return "\n".join(
+            [
+                "if (mt_kb != 0u) {  // contributor: hand the partial sums to the owner",
+                f"    mt_f32x4* mt_part4 = reinterpret_cast<mt_f32x4*>(mt_ws_part(mt_ws, blockIdx.x, {tile_floats}u));",
+                *("    " + x for x in stores),
+                "    mt_sk_signal(mt_ws_flag(mt_ws, blockIdx.x));",
+                "    continue;",
+                "}",
+                "if (mt_ke != mt_chunks) {  // owner of a split tile: add the later ranges' partial sums",
+                "    const unsigned long long mt_tend = (unsigned long long)(mt_t - mt_sk.dp + 1u) * mt_chunks;",
+                "    // no range is empty (stream-K needs as many units as workgroups), so the",
+                "    // contributors are the workgroups at offsets 1 .. mt_nc below this one",
+                "    unsigned mt_nc = 0u;",
+                "    for (unsigned mt_c = mt_sk.contributor(1u, mt_tend); mt_c != 0u;"
+                " mt_c = mt_sk.contributor(mt_c + 1u, mt_tend)) {",
+                "        mt_sk_wait(mt_ws_flag(mt_ws, blockIdx.x - mt_c), mt_ws_error(mt_ws));",
+                "        mt_nc = mt_c;",
+                "    }",
+                *("    " + x for x in adds),
+                "}",
             ]
         )
 
@@ -218,11 +346,14 @@ class MatmulMainloopFragment:
     in iteration kt only after every lane passed the barrier that ended
     iteration kt-1, the last reader of b.
 
-    ``persistent`` (inside a persistent tile loop): the buffer index is the
-    running ``mt_stage``, flipped after every chunk of every tile; only the
-    first tile loads chunk 0 before its loop, and the last iteration of each
-    tile loads chunk 0 of the next tile (``mt_next_m0/n0``) into the other
-    buffer, so the same one-barrier-per-chunk argument spans tiles."""
+    ``persistent`` (inside a persistent tile loop): the loop runs over the
+    item's chunks ``[mt_kb, mt_ke)`` (every chunk of the tile unless a
+    stream-K schedule split it); the buffer index is the running
+    ``mt_stage``, flipped after every chunk of every item; only the first
+    item loads its first chunk before its loop, and the last iteration of
+    each item loads the next item's first chunk (``mt_next_m0/n0/kb``) into
+    the other buffer, so the same one-barrier-per-chunk argument spans
+    items."""
 
     tile_K: int
     fragments: tuple[KernelFragment, ...]
@@ -283,25 +414,24 @@ class MatmulMainloopFragment:
         return "{\n" + textwrap.indent("\n".join(body), "    ") + "\n}"
 
     def _render_persistent(self, loads, computes, body: list[str]) -> str:
-        kvar, tk = self.K_dim_var, self.tile_K
+        tk = self.tile_K
         body += [
-            f"const unsigned n_chunks = ({kvar} + {tk - 1}u) / {tk}u;",
             "if (mt_first_tile) {",
-            "    const unsigned k_chunk = 0u;",
+            f"    const unsigned k_chunk = mt_kb * {tk}u;",
             *[f"    {ld.render_fetch()}" for ld in loads],
             *[f"    {ld.render_commit('mt_stage')}" for ld in loads],
             "    __syncthreads();",
             "}",
-            "for (unsigned kt = 0; kt < n_chunks; ++kt) {",
+            "for (unsigned kt = mt_kb; kt < mt_ke; ++kt) {",
             "    const unsigned cur = mt_stage;",
-            "    const bool more = kt + 1u < n_chunks;",
+            "    const bool more = kt + 1u < mt_ke;",
             "    if (more) {",
             f"        const unsigned k_chunk = (kt + 1u) * {tk}u;",
             *[f"        {ld.render_fetch()}" for ld in loads],
             "    } else if (mt_has_next) {",
             "        const unsigned tile_m0 = mt_next_m0;",
             "        const unsigned tile_n0 = mt_next_n0;",
-            "        const unsigned k_chunk = 0u;",
+            f"        const unsigned k_chunk = mt_next_kb * {tk}u;",
             *[f"        {ld.render_fetch()}" for ld in loads],
             "    }",
             *[f"    {c.render_stage('cur')}" for c in computes],

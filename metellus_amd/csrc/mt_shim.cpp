@@ -82,7 +82,15 @@ struct State {
     std::unordered_map<void*, size_t> host_cap;
     std::multimap<size_t, void*> host_free;
     size_t host_cached = 0;
+    // Workspace of stream-K kernels (a registry buffer the shim owns).
+    uint64_t ws_handle = 0;
+    size_t ws_bytes = 0;
 };
+
+// Workspace layout shared with the device library (MT_WS_HEAD): flag words,
+// the last of them the error word, then the partial tiles.
+constexpr size_t kWsHeadBytes = 1024 * sizeof(uint32_t);
+constexpr size_t kWsErrorOffset = 1023 * sizeof(uint32_t);
 
 constexpr size_t kHostGranule = size_t(64) << 10;     // pinned blocks are multiples of 64 KiB
 constexpr size_t kHostCacheLimit = size_t(1) << 30;   // at most 1 GiB of returned blocks kept
@@ -285,6 +293,7 @@ int mt_alloc(size_t nbytes, uint64_t* handle) {
 int mt_free(uint64_t handle, int* existed) {
     State& s = state();
     std::lock_guard<std::mutex> lock(s.mu);
+    if (handle != 0 && handle == s.ws_handle) return fail("mt_free: the workspace belongs to the shim");
     auto it = s.buffers.find(handle);
     if (it == s.buffers.end()) {
         if (existed) *existed = 0;
@@ -487,6 +496,50 @@ int mt_launch(uint64_t kernel, const uint64_t* buffers, int nbuf, const uint32_t
         MT_HIP(hipEventElapsedTime(&t, s.ev_start, s.ev_stop));
         if (ms) *ms = t;
     }
+    return 0;
+}
+
+int mt_workspace(size_t nbytes, uint64_t* handle) {
+    if (!handle) return fail("mt_workspace: null output");
+    if (nbytes < kWsHeadBytes) return fail("mt_workspace: a workspace holds at least its 4096-byte head");
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    if (nbytes > s.ws_bytes) {
+        if (s.ws_handle) {
+            // Stream-ordered: kernels already queued on the old one finish first.
+            MT_HIP(hipFreeAsync(s.buffers[s.ws_handle].ptr, s.stream));
+            s.buffers.erase(s.ws_handle);
+            s.ws_handle = 0;
+            s.ws_bytes = 0;
+        }
+        void* p = nullptr;
+        MT_HIP(hipMallocAsync(&p, nbytes, s.stream));
+        MT_HIP(hipMemsetAsync(p, 0, kWsHeadBytes, s.stream));  // flags and error word start at 0
+        s.ws_handle = s.next_buffer++;
+        s.buffers.emplace(s.ws_handle, Buffer{p, nbytes});
+        s.ws_bytes = nbytes;
+    }
+    *handle = s.ws_handle;
+    return 0;
+}
+
+int mt_workspace_check(uint32_t* error) {
+    if (!error) return fail("mt_workspace_check: null output");
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    *error = 0;
+    if (!s.ws_handle) return 0;
+    char* p = static_cast<char*>(s.buffers[s.ws_handle].ptr);
+    uint32_t word = 0;
+    MT_HIP(hipMemcpyAsync(&word, p + kWsErrorOffset, sizeof(word), hipMemcpyDeviceToHost, s.stream));
+    MT_HIP(hipStreamSynchronize(s.stream));
+    if (word != 0) {
+        // A wait gave up: its flags may be stale, so start the next launch clean.
+        MT_HIP(hipMemsetAsync(p, 0, kWsHeadBytes, s.stream));
+        MT_HIP(hipStreamSynchronize(s.stream));
+    }
+    *error = word;
     return 0;
 }
 

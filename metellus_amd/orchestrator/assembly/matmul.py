@@ -12,7 +12,10 @@ applied to the accumulator registers (both ``MATMUL_EPILOGUE_REGISTER`` and
 ``MATMUL_EPILOGUE_TG``; the label records the reference's decision), then a
 direct store.  LDS holds only the A and B chunks.  When the output tiles
 outnumber the workgroups resident at once, the grid is instead
-``(P, 1, 1)`` workgroups looping over tiles (``PersistentTiles``).
+``(P, 1, 1)`` workgroups looping over tiles (``PersistentTiles``); when
+the tiles are not a whole number of rounds, the last round is split by
+k-chunks (stream-K) through a workspace the runtime passes as the last
+kernel parameter.
 """
 
 from __future__ import annotations
@@ -26,6 +29,7 @@ from metellus_amd.compute.matmul.config import (
     is_aligned_shape,
     persistent_workgroups,
     select_tile_config,
+    uses_stream_k,
 )
 from metellus_amd.compute.matmul.matmul import (
     MatmulComputeFragment,
@@ -36,7 +40,9 @@ from metellus_amd.compute.matmul.matmul import (
     MatmulTileMappingFragment,
     PersistentLoopEndFragment,
     PersistentTiles,
+    StreamKFixupFragment,
     ThreadIndexFragment,
+    stream_k_workspace_bytes,
 )
 from metellus_amd.memory.memory import TgLoadFragment
 from metellus_amd.orchestrator.assembly.decision import DecisionView
@@ -201,7 +207,9 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
     b_load = operand_load(name="load_B_tile", src=src_b, dst="B_tile", tile=tile, side="b",
                           M=M, K=K, N=N, aligned=aligned, prologue=pro_b)
     n_persistent = persistent_workgroups(M, N, tile, batch)
-    persistent = PersistentTiles(tile.tile_M, tile.tile_N) if n_persistent else None
+    stream_k = uses_stream_k(M, K, N, tile, n_persistent, batch)
+    persistent = PersistentTiles(tile.tile_M, tile.tile_N, stream_k=stream_k, tile_K=tile.tile_K) \
+        if n_persistent else None
     mainloop = MatmulMainloopFragment(
         tile_K=tile.tile_K,
         fragments=(a_load, b_load, BarrierFragment("inputs_ready"), MatmulComputeFragment(config),
@@ -215,6 +223,7 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         ThreadIndexFragment(tile),
         MatmulSetupFragment(config),
         mainloop,
+        *((StreamKFixupFragment(config),) if stream_k else ()),
         store,
         *((PersistentLoopEndFragment(),) if persistent else ()),
     )
@@ -226,6 +235,7 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         tg_y=1,
         threadgroup_decls=(lds_decl("A_tile", tile.a_tile_shape()), lds_decl("B_tile", tile.b_tile_shape())),
         helpers=tuple(helpers),
+        workspace_bytes=stream_k_workspace_bytes(tile.tile_M, tile.tile_N, n_persistent) if stream_k else 0,
     )
     return KernelGroup(
         kernel=Kernel(fragments=fragments, ctx=ctx),

@@ -46,6 +46,8 @@ EXPORTED_SYMBOLS = (
     "mt_launch",
     "mt_sync",
     "mt_cache_stats",
+    "mt_workspace",
+    "mt_workspace_check",
 )
 
 _lib = None
@@ -101,6 +103,8 @@ def _load():
             ),
             "mt_sync": ([], ctypes.c_int),
             "mt_cache_stats": ([ctypes.POINTER(_u64), ctypes.POINTER(_u64)], ctypes.c_int),
+            "mt_workspace": ([ctypes.c_size_t, ctypes.POINTER(_u64)], ctypes.c_int),
+            "mt_workspace_check": ([ctypes.POINTER(ctypes.c_uint32)], ctypes.c_int),
         }
         for name, (args, res) in sig.items():
             fn = getattr(lib, name)
@@ -234,6 +238,25 @@ def compile_only(source: str, options: str = "", target: str = "gfx950") -> int:
     return n.value
 
 
+def workspace_handle(nbytes: int) -> int:
+    """Handle of the shim's device workspace (at least ``nbytes``)."""
+    h = _u64(0)
+    _check(_load().mt_workspace(int(nbytes), ctypes.byref(h)))
+    return h.value
+
+
+def check_workspace() -> None:
+    """Raise if a stream-K workgroup gave up waiting for a partial tile since
+    the last check (the results of that launch are invalid)."""
+    err = ctypes.c_uint32(0)
+    _check(_load().mt_workspace_check(ctypes.byref(err)))
+    if err.value:
+        raise RuntimeError(
+            "stream-K matmul: a workgroup gave up waiting for another workgroup's partial tile; "
+            "the results of that launch are invalid (the workspace flags were reset)"
+        )
+
+
 def launch(
     kernel: int,
     buffers,
@@ -242,10 +265,15 @@ def launch(
     grid,
     threads,
     timed: bool = False,
+    workspace: int = 0,
 ) -> float | None:
     """Launch ``kernel``; buffers are handles (or objects with ``.handle``).
-    Returns the kernel time in ms when ``timed``."""
+    ``workspace`` > 0: the kernel takes the shim's workspace (at least that
+    many bytes) as its last parameter.  Returns the kernel time in ms when
+    ``timed``."""
     handles = [_handle_of(b) for b in buffers]
+    if workspace:
+        handles.append(workspace_handle(workspace))
     nb = len(handles)
     bufs = (_u64 * max(nb, 1))(*handles)
     dims_l = [int(d) for d in dims]

@@ -136,6 +136,11 @@ class Kernel:
         return self.ctx.dims
 
     @property
+    def workspace_bytes(self) -> int:
+        """Device workspace the kernel takes as its last parameter (0: none)."""
+        return self.ctx.workspace_bytes
+
+    @property
     def handle(self) -> int:
         if self._handle is None:
             from metellus_amd.runtime import hip_backend
@@ -152,6 +157,8 @@ class Kernel:
         (launch with grid z = batch size)."""
         if self.ctx.batched:
             return self
+        if self.ctx.workspace_bytes:
+            raise ValueError(f"{self.function_name}: a kernel with a workspace (stream-K) is not batched")
         cached = getattr(self, "_batched", None)
         if cached is None:
             import dataclasses
@@ -193,6 +200,7 @@ class Dispatch:
             self.grid,
             self.threads,
             timed=self.time_key is not None,
+            workspace=self.kernel.workspace_bytes,
         )
         if self.time_key is not None:
             env[self.time_key] = float(t)
@@ -207,6 +215,10 @@ class Runtime:
             env = {}
         for step in self.fragments:
             step.execute(env)
+        if any(isinstance(s, Dispatch) and s.kernel.workspace_bytes for s in self.fragments):
+            from metellus_amd.runtime import hip_backend
+
+            hip_backend.check_workspace()  # raises if a stream-K wait gave up
         return env
 
     def __add__(self, other: "Runtime") -> "Runtime":

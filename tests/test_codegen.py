@@ -2,6 +2,8 @@
 generated source (no GPU): where matmul prologues are applied, and how
 batched kernels address their per-program buffers."""
 
+import pytest
+
 from metellus_amd.api import compile_program
 from metellus_amd.runtime import hip_backend
 from tests import gpu_cases
@@ -67,12 +69,36 @@ def test_persistent_loop_only_when_tiles_exceed_one_round(monkeypatch):
     assert "mt_t += gridDim.x" not in gemm.kernel.source
 
     monkeypatch.setattr(config, "PERSISTENT_CAPACITY", 2)
+    monkeypatch.setattr(config, "STREAM_K", False)
     g = compile_program(gpu_cases.plain_matmul(192, 96, 320))[0]
     assert g.grid == (2, 1, 1)
     src = g.kernel.source
     assert "for (unsigned mt_t = blockIdx.x; mt_t < mt_tiles; mt_t += gridDim.x) {" in src
     assert "} else if (mt_has_next) {" in src and "}  // persistent tile loop" in src
+    assert g.kernel.workspace_bytes == 0 and "mt_ws" not in src.split('extern "C"')[1]
     assert hip_backend.compile_only(src) > 0
+
+
+def test_stream_k_kernel_takes_the_workspace_last(monkeypatch):
+    from metellus_amd.compute.matmul import config
+    from metellus_amd.compute.matmul.matmul import stream_k_workspace_bytes
+
+    # C4's X @ W1: 688 tiles of 256x256 on 256 resident workgroups
+    g = compile_program(gpu_cases.mlp_block(4096, 4096, 11008))[0]
+    assert g.grid == (256, 1, 1)
+    assert g.kernel.workspace_bytes == stream_k_workspace_bytes(256, 256, 256)
+    body = g.kernel.source.split('extern "C"')[1]
+    assert "const mt_dims dims,\n    float* mt_ws\n)" in body
+    assert "mt_sk.init(mt_tiles, mt_chunks, gridDim.x, blockIdx.x);" in body
+    assert "mt_sk_signal(" in body and "mt_sk_wait(" in body
+    assert hip_backend.compile_only(g.kernel.source) > 0
+    with pytest.raises(ValueError, match="not batched"):
+        g.kernel.batched()
+    # whole rounds keep the plain loop; the switch turns stream-K off
+    assert compile_program(gpu_cases.plain_matmul(4096, 4096, 4096))[0].kernel.workspace_bytes == 0
+    monkeypatch.setattr(config, "STREAM_K", False)
+    g = compile_program(gpu_cases.mlp_block(4096, 4096, 11008))[0]
+    assert g.kernel.workspace_bytes == 0 and "mt_t += gridDim.x" in g.kernel.source
 
 
 def test_persistent_batched_grid_splits_capacity_over_programs(monkeypatch):

@@ -2,7 +2,9 @@
 every matmul kernel loop over several tiles per workgroup (with the
 cross-tile prefetch).  The per-tile arithmetic is unchanged, so the results
 must be bit-identical to the one-tile-per-workgroup launch, and within the
-matmul bar of the oracle."""
+matmul bar of the oracle.  Stream-K (which splits the last partial round by
+k-chunks and so sums those tiles in another order) is switched off here and
+tested in test_gpu_stream_k.py."""
 
 from __future__ import annotations
 
@@ -23,6 +25,7 @@ def _both(make, capacity, monkeypatch, runner=run):
     classic = runner(make())
     monkeypatch.setattr(config, "PERSISTENT", True)
     monkeypatch.setattr(config, "PERSISTENT_CAPACITY", capacity)
+    monkeypatch.setattr(config, "STREAM_K", False)
     persistent = runner(make())
     return classic, persistent
 
