@@ -181,13 +181,13 @@ def resident_workgroups(t: TileConfig, anchors: int = 1) -> int:
     return max(1, min(by_lds, by_vgpr))
 
 
-def persistent_workgroups(M: int, N: int, t: TileConfig, batch: int = 1) -> int | None:
+def persistent_workgroups(M: int, N: int, t: TileConfig, batch: int = 1, anchors: int = 1) -> int | None:
     """Workgroups per problem for a persistent tile loop, or None when every
     tile of every problem gets a resident workgroup in one round anyway."""
     if not PERSISTENT or t.stages != 2:
         return None
     tiles = ceil_div(M, t.tile_M) * ceil_div(N, t.tile_N)
-    capacity = PERSISTENT_CAPACITY or NUM_CUS * resident_workgroups(t)
+    capacity = PERSISTENT_CAPACITY or NUM_CUS * resident_workgroups(t, anchors)
     if tiles * batch <= capacity:
         return None
     return min(tiles, max(1, capacity // batch))

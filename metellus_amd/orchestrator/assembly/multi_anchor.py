@@ -11,12 +11,21 @@ diamond runs one mainloop that loads the shared A chunk once and both B
 chunks; otherwise two mainloops run back to back, and their LDS tiles have
 disjoint lifetimes, so the aliasing pass gives A1/B1 the storage of A0/B0.
 The merge op is applied per register and stored directly -- no C tiles.
+The diamond takes the persistent tile loop (and stream-K for a partial last
+round, handing over both accumulator sets) like a single matmul; the
+two-mainloop form keeps one tile per workgroup.
 """
 
 from __future__ import annotations
 
 from metellus_amd.compute.fragments import BarrierFragment, CodegenContext, lds_decl
-from metellus_amd.compute.matmul.config import grid_for, is_aligned_shape, select_tile_config
+from metellus_amd.compute.matmul.config import (
+    grid_for,
+    is_aligned_shape,
+    persistent_workgroups,
+    select_tile_config,
+    uses_stream_k,
+)
 from metellus_amd.compute.matmul.matmul import (
     MatmulComputeFragment,
     MatmulConfig,
@@ -24,7 +33,11 @@ from metellus_amd.compute.matmul.matmul import (
     MatmulMainloopFragment,
     MatmulSetupFragment,
     MatmulTileMappingFragment,
+    PersistentLoopEndFragment,
+    PersistentTiles,
+    StreamKFixupFragment,
     ThreadIndexFragment,
+    stream_k_workspace_bytes,
 )
 from metellus_amd.orchestrator.assembly.decision import DecisionView
 from metellus_amd.orchestrator.assembly.expressions import ChainCode
@@ -106,6 +119,10 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
         return operand_load(name=f"load_B{i}_tile", src=src_b[i], dst=f"B{i}_tile", tile=tile, side="b",
                             M=M, K=ks[i], N=N, aligned=aligned, k_limit=kvars[i], prologue=tf_b[i])
 
+    n_persistent = persistent_workgroups(M, N, tile, batch, anchors=2) if shared else None
+    stream_k = uses_stream_k(M, K0, N, tile, n_persistent, batch)
+    persistent = PersistentTiles(tile.tile_M, tile.tile_N, stream_k=stream_k, tile_K=tile.tile_K) \
+        if n_persistent else None
     if shared:
         a_load = operand_load(name="load_A_tile", src=src_a[0], dst="A_tile", tile=tile, side="a",
                               M=M, K=K0, N=N, aligned=aligned, k_limit="K")
@@ -122,6 +139,7 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
                     BarrierFragment("compute_done"),
                 ),
                 K_dim_var="K",
+                persistent=persistent is not None,
             )
         ]
     else:
@@ -145,12 +163,14 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
 
     store = MatmulEpilogueStoreFragment(configs[0], value_expr=value_expr, suffixes=suffixes, check=not aligned)
     fragments = (
-        MatmulTileMappingFragment(),
+        MatmulTileMappingFragment(persistent),
         ThreadIndexFragment(tile),
         MatmulSetupFragment(configs[0], accumulator_suffix=suffixes[0]),
         MatmulSetupFragment(configs[1], accumulator_suffix=suffixes[1], emit_thread_coords=False),
         *mainloops,
+        *((StreamKFixupFragment(configs[0], suffixes=suffixes),) if stream_k else ()),
         store,
+        *((PersistentLoopEndFragment(),) if persistent else ()),
     )
     decls = []
     if shared:
@@ -170,12 +190,13 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
         tg_y=1,
         threadgroup_decls=tuple(decls),
         helpers=tuple(helpers),
+        workspace_bytes=stream_k_workspace_bytes(tile.tile_M, tile.tile_N, n_persistent, anchors=2) if stream_k else 0,
     )
     return KernelGroup(
         kernel=Kernel(fragments=fragments, ctx=ctx),
         bindings=(*keys, out_key, *extras.bindings),
         dims=dim_values,
-        grid=grid_for(M, N, tile),
+        grid=(n_persistent, 1, 1) if n_persistent else grid_for(M, N, tile),
         threads=(tile.tg_x, 1, 1),
         ops=decision.ops,
         strategy=decision.strategy,

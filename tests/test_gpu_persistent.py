@@ -80,3 +80,11 @@ def test_batched_attention_bit_identical(monkeypatch):
         assert p.groups[0].grid == (1, 1, 1)  # capacity 4 over 3 programs: one looping workgroup each
         np.testing.assert_array_equal(p.env["O"], c.env["O"])
         np.testing.assert_array_equal(p.env["m1"], c.env["m1"])
+
+
+def test_diamond_bit_identical(monkeypatch):
+    """The shared-A multi-anchor kernel in a persistent tile loop."""
+    classic, persistent = _both(lambda: gpu_cases.mlp_block(512, 256, 704, seed=6, diamond=True), 3, monkeypatch)
+    assert len(persistent.groups) == 1 and persistent.groups[0].grid == (3, 1, 1)
+    assert classic.groups[0].grid[0] * classic.groups[0].grid[1] > 3
+    np.testing.assert_array_equal(persistent.env["z"], classic.env["z"])

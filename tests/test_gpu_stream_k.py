@@ -127,3 +127,25 @@ def test_c4_x_w1_at_full_size():
     ref = x[rows] @ w1
     tol = 1e-4 * np.sqrt(4096) * (np.abs(x[rows]) @ np.abs(w1)) + 1e-30
     assert np.all(np.abs(res.env["h1"][rows] - ref) <= tol)
+
+
+@pytest.mark.parametrize("mdh,capacity", [((512, 256, 704), 5), ((700, 300, 900), 7)])
+def test_diamond_two_accumulator_sets(mdh, capacity, monkeypatch):
+    """(X @ W1) * (X @ W2) in one kernel: both accumulator sets of a split
+    tile are handed over."""
+    M, D, H = mdh
+    _stream_k(monkeypatch, capacity)
+    ops = gpu_cases.mlp_block(M, D, H, seed=5, diamond=True)
+    first = run(ops)
+    assert len(first.groups) == 1
+    g = first.groups[0]
+    assert g.grid == (capacity, 1, 1) and g.kernel.workspace_bytes > 0
+    second = run(gpu_cases.mlp_block(M, D, H, seed=5, diamond=True))
+    np.testing.assert_array_equal(first.env["z"], second.env["z"])
+    ref = evaluate(ops)
+    x, w1, w2 = (ops.uploads[k].astype(np.float64) for k in ("X", "W1", "W2"))
+    h1, h2 = ref["h1"], ref["h2"]
+    # |h1 h2 - z| <= |h2| tol(h1) + |h1| tol(h2) + tol(h1) tol(h2), tol = the matmul bar
+    t1, t2 = matmul_tolerance(x, w1), matmul_tolerance(x, w2)
+    bound = np.abs(h2) * t1 + np.abs(h1) * t2 + t1 * t2 + np.abs(h1 * h2) * 2.0 ** -23 + 1e-30
+    assert np.all(np.abs(first.env["z"] - h1 * h2) <= bound)
