@@ -365,6 +365,86 @@ def cpu_baseline_c2(ops, budget_s: float = 10.0) -> dict:
     }
 
 
+def _blas_threads() -> int:
+    try:
+        import threadpoolctl
+
+        info = [p for p in threadpoolctl.threadpool_info() if p.get("user_api") == "blas"]
+        if info:
+            return int(info[0]["num_threads"])
+    except ImportError:
+        pass
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_baseline_config(label: str, made, per_kernel: list[dict], budget_s: float = 3.0) -> dict | None:
+    """Time one whole configuration on the host CPU in float32: the
+    oracle's elementwise ops (NumPy ufuncs, one thread), NumPy's float32 row
+    reductions, and NumPy float32 matmuls (OpenBLAS sgemm on its thread
+    pool).  At least two evaluations after one warm-up, about ``budget_s``.
+    Throughput uses the configuration's algorithmic work: the matmul flops
+    when it has matmuls, else the kernels' algorithmic bytes."""
+    from oracle.ir_eval import apply_elementwise
+
+    f32 = np.float32
+    sig = lambda t: apply_elementwise("recip", apply_elementwise("add", apply_elementwise("exp", apply_elementwise("negate", t)), f32(1.0)))
+
+    def softmax_rows(x):
+        m = np.max(x, axis=-1, keepdims=True)
+        e = apply_elementwise("exp", apply_elementwise("subtract", x, m))
+        return apply_elementwise("div", e, np.sum(e, axis=-1, keepdims=True, dtype=f32))
+
+    if label.startswith("C3"):
+        x = made.uploads["x"]
+        once = lambda: softmax_rows(x)
+    elif label.startswith("matmul"):
+        a, b = made.uploads["A"], made.uploads["B"]
+        once = lambda: a @ b
+    elif label.startswith("C4"):
+        u = made.uploads
+
+        def once():
+            h1, h2 = u["X"] @ u["W1"], u["X"] @ u["W2"]
+            if "W3" not in u:  # the diamond variant stops at the product
+                return apply_elementwise("mul", h1, h2)
+            z = apply_elementwise("mul", apply_elementwise("mul", h1, sig(h1)), h2)
+            return z @ u["W3"]
+
+    elif label.startswith("C5"):
+        q, k, v = (np.stack([p.uploads[n] for p in made]) for n in "QKV")
+        kt = k.transpose(0, 2, 1)
+        scale = f32(1.0 / np.sqrt(q.shape[-1]))
+        once = lambda: softmax_rows(apply_elementwise("mul", q @ kt, scale)) @ v
+    else:
+        return None
+    mine = [k for k in per_kernel if k["config"] == label]
+    if any(k["bound"] == "mfma" for k in mine):
+        work, unit, div = sum(k["work"] for k in mine if k["bound"] == "mfma"), "TFLOP/s", 1e12
+    else:
+        work, unit, div = sum(k["work"] for k in mine), "GB/s", 1e9
+    once()
+    times, t0 = [], time.perf_counter()
+    while len(times) < 2 or time.perf_counter() - t0 < budget_s:
+        s = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - s)
+    med = float(np.median(times))
+    gpu_ms = sum(k["ms_mean"] for k in mine)
+    has_mm = unit == "TFLOP/s"
+    return {
+        "config": label,
+        "value": round(work / med / div, 4),
+        "unit": unit,
+        "cores": _blas_threads() if has_mm else 1,
+        "kind": "port",
+        "sample": f"whole configuration, full inputs, NumPy float32 ({'OpenBLAS sgemm + ' if has_mm else ''}"
+        f"single-thread ufuncs), {len(times)} evaluations, median {med*1e3:.1f} ms",
+        "ms": round(med * 1e3, 3),
+        "gpu_kernels_ms": round(gpu_ms, 4),
+        "gpu_over_cpu": round(med * 1e3 / gpu_ms, 1) if gpu_ms > 0 else None,
+    }
+
+
 def fragment_benches(steps: int, flusher) -> list[dict]:
     """The reference's fragment-level benches (tests/bench_init.py,
     bench_reduction.py, bench_elementwise.py, bench_matmul.py) at their own
@@ -512,6 +592,7 @@ def main() -> int:
     only = args.only
     line = None
     per_config: list[dict] = []
+    cpu_configs: list[dict] = []
     if only in (None, "c2"):
         log("[bench] C2 sigmoid chain 4096x4096: preparing")
         prep = time_prep = Prepared(_c2())
@@ -607,8 +688,16 @@ def main() -> int:
             prep = PreparedBatch(made) if isinstance(made, list) else Prepared(made)
             per_config += time_kernels(prep, extra_steps, 2, flush, label)
             prep.release()
+            if not args.no_cpu:
+                cpu = cpu_baseline_config(label, made, per_config)
+                if cpu is not None:
+                    cpu_configs.append(cpu)
+                    log(f"[bench] {label} CPU: {cpu['value']} {cpu['unit']} on {cpu['cores']} threads "
+                        f"({cpu['ms']:.1f} ms; GPU kernels {cpu['gpu_kernels_ms']:.3f} ms)")
     if line is None:
         line = {"metric": "fused-kernel fp32 TFLOP/s & HBM GB/s (% of roofline), 1×MI355X", "value": None}
+    if cpu_configs:
+        line.setdefault("cpu_baseline", {})["per_config"] = cpu_configs
     line["per_kernel"] = per_config
     print(json.dumps(line), flush=True)
     return 0
