@@ -78,8 +78,10 @@ int mt_host_free(void* ptr);
 /* First half of run_kernel (reference: src/metal_backend.mm:178-207):
  * compile `source` with hiprtc for the device's target, load it and look up
  * `function_name`.  Code objects are cached in memory (and on disk unless
- * MT_KERNEL_CACHE=0) by the exact (source, function, options, target) key,
- * so repeated dispatches do not recompile.  `options` is a space-separated
+ * MT_KERNEL_CACHE=0) by the exact (source, function, options, target,
+ * hiprtc version) key, so repeated dispatches do not recompile; a disk entry
+ * stores its key and is used only when that key matches in full.
+ * `options` is a space-separated
  * list appended to the defaults (-O3 -std=c++17 -ffp-contract=off, packed
  * fp32 ops disabled). */
 int mt_compile(const char* source, const char* function_name, const char* options, uint64_t* kernel);

@@ -31,6 +31,13 @@ class TileConfig:
     b_pad: int = 4
     stages: int = 2
     c_pad: int = 4  # row padding of an LDS C tile (MatmulAccumToTgFragment)
+    # LDS layouts of the operand tiles.  "pad": rows padded by a_pad / b_pad,
+    # filled from registers.  Filled by direct-to-LDS loads instead (dense
+    # rows): A "swz" = [tile_M][tile_K] with XOR-swizzled 16-byte slots;
+    # B "dense" = [tile_K][tile_N]; B "nswz" = n-major [tile_N][tile_K],
+    # swizzled like A (a transposed view such as K^T, read along K).
+    a_layout: str = "pad"
+    b_layout: str = "pad"
 
     @property
     def num_threads(self) -> int:
@@ -62,16 +69,24 @@ class TileConfig:
 
     @property
     def lda(self) -> int:
-        return self.tile_K + self.a_pad
+        return self.tile_K if self.a_layout == "swz" else self.tile_K + self.a_pad
 
     @property
     def ldb(self) -> int:
+        """Row pitch of the B tile: along N (k-major layouts) or along K
+        (the n-major layout)."""
+        if self.b_layout == "dense":
+            return self.tile_N
+        if self.b_layout == "nswz":
+            return self.tile_K
         return self.tile_N + self.b_pad
 
     def a_tile_shape(self) -> tuple[int, ...]:
         return (self.stages, self.tile_M, self.lda)
 
     def b_tile_shape(self) -> tuple[int, ...]:
+        if self.b_layout == "nswz":
+            return (self.stages, self.tile_N, self.tile_K)
         return (self.stages, self.tile_K, self.ldb)
 
     def validate(self) -> None:
@@ -83,6 +98,10 @@ class TileConfig:
             raise ValueError(f"A tile row pitch must be a multiple of 4 floats (128-bit reads): {self}")
         if self.num_threads > 1024:
             raise ValueError(f"at most 1024 lanes per workgroup: {self}")
+        if self.a_layout not in ("pad", "swz") or self.b_layout not in ("pad", "dense", "nswz"):
+            raise ValueError(f"unknown operand tile layout: {self}")
+        if (self.a_layout == "swz" or self.b_layout == "nswz") and self.tile_K not in (16, 32):
+            raise ValueError(f"swizzled tiles are defined for tile_K 16 and 32: {self}")
 
 
 def ceil_div(a: int, b: int) -> int:

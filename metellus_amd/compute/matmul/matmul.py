@@ -306,9 +306,17 @@ class MatmulComputeFragment:
         t = self.config.tile
         at, bt = self.config.a_tile_name, self.config.b_tile_name
         a_ptr = f"&{at}[{stage}][wave_m0][0]" if stage is not None else f"&{at}[wave_m0][0]"
-        b_ptr = f"&{bt}[{stage}][0][wave_n0]" if stage is not None else f"&{bt}[0][wave_n0]"
+        if t.b_layout == "nswz":  # n-major B: the wave's first column is a row
+            b_ptr = f"&{bt}[{stage}][wave_n0][0]" if stage is not None else f"&{bt}[wave_n0][0]"
+        else:
+            b_ptr = f"&{bt}[{stage}][0][wave_n0]" if stage is not None else f"&{bt}[0][wave_n0]"
+        flags = ""
+        if t.a_layout != "pad" or t.b_layout == "nswz":
+            aswz = "true" if t.a_layout == "swz" else "false"
+            bnm = "true" if t.b_layout == "nswz" else "false"
+            flags = f", {aswz}, {bnm}"
         return (
-            f"mt_mfma_tile<{t.WM}, {t.WN}, {t.tile_K}, {t.lda}, {t.ldb}>"
+            f"mt_mfma_tile<{t.WM}, {t.WN}, {t.tile_K}, {t.lda}, {t.ldb}{flags}>"
             f"({a_ptr}, {b_ptr}, acc{self.accumulator_suffix}, lane);"
         )
 
@@ -368,12 +376,21 @@ class MatmulMainloopFragment:
     def _computes(self):
         return [f for f in self.fragments if isinstance(f, MatmulComputeFragment)]
 
+    def _sync(self, loads) -> list[str]:
+        """End of a chunk: the barrier, preceded by a wait for this wave's
+        direct-to-LDS loads when there are any (the compiler does not track
+        them)."""
+        dma = ["__builtin_amdgcn_s_waitcnt(0);"] if any(getattr(ld, "is_dma", False) for ld in loads) else []
+        return [*dma, "__syncthreads();"]
+
     def render(self, ctx: CodegenContext) -> str:
         loads, computes = self._loads(), self._computes()
         stages = max((ld.stages for ld in loads), default=1)
         kvar = self.K_dim_var
         tk = self.tile_K
         body: list[str] = [ld.render_decl() for ld in loads]
+        if stages == 1 and any(getattr(ld, "is_dma", False) for ld in loads):
+            raise ValueError("direct-to-LDS loads need double-buffered LDS tiles")
         if stages == 1:
             body += [
                 f"for (unsigned k_chunk = 0; k_chunk < {kvar}; k_chunk += {tk}u) {{",
@@ -389,56 +406,55 @@ class MatmulMainloopFragment:
             if stages != 2:
                 raise ValueError("a persistent tile loop needs double-buffered LDS tiles")
             return self._render_persistent(loads, computes, body)
+        sync = self._sync(loads)
         body += [
             f"const unsigned n_chunks = ({kvar} + {tk - 1}u) / {tk}u;",
             "{",
             "    const unsigned k_chunk = 0u;",
-            *[f"    {ld.render_fetch()}" for ld in loads],
+            *[f"    {ld.render_fetch(stage='0')}" for ld in loads],
             "}",
-            *[ld.render_commit("0") for ld in loads],
-            "__syncthreads();",
+            *_nonempty(ld.render_commit("0") for ld in loads),
+            *sync,
             "for (unsigned kt = 0; kt < n_chunks; ++kt) {",
             "    const unsigned cur = kt & 1u;",
             "    const bool more = kt + 1u < n_chunks;",
             "    if (more) {",
             f"        const unsigned k_chunk = (kt + 1u) * {tk}u;",
-            *[f"        {ld.render_fetch()}" for ld in loads],
+            *[f"        {ld.render_fetch(stage='cur ^ 1u')}" for ld in loads],
             "    }",
             *[f"    {c.render_stage('cur')}" for c in computes],
-            "    if (more) {",
-            *[f"        {ld.render_commit('cur ^ 1u')}" for ld in loads],
-            "    }",
-            "    __syncthreads();",
+            *_guarded("    if (more) {", [f"        {c}" for c in _nonempty(ld.render_commit("cur ^ 1u") for ld in loads)]),
+            *[f"    {x}" for x in sync],
             "}",
         ]
         return "{\n" + textwrap.indent("\n".join(body), "    ") + "\n}"
 
     def _render_persistent(self, loads, computes, body: list[str]) -> str:
         tk = self.tile_K
+        sync = self._sync(loads)
         body += [
             "if (mt_first_tile) {",
             f"    const unsigned k_chunk = mt_kb * {tk}u;",
-            *[f"    {ld.render_fetch()}" for ld in loads],
-            *[f"    {ld.render_commit('mt_stage')}" for ld in loads],
-            "    __syncthreads();",
+            *[f"    {ld.render_fetch(stage='mt_stage')}" for ld in loads],
+            *[f"    {c}" for c in _nonempty(ld.render_commit("mt_stage") for ld in loads)],
+            *[f"    {x}" for x in sync],
             "}",
             "for (unsigned kt = mt_kb; kt < mt_ke; ++kt) {",
             "    const unsigned cur = mt_stage;",
             "    const bool more = kt + 1u < mt_ke;",
             "    if (more) {",
             f"        const unsigned k_chunk = (kt + 1u) * {tk}u;",
-            *[f"        {ld.render_fetch()}" for ld in loads],
+            *[f"        {ld.render_fetch(stage='cur ^ 1u')}" for ld in loads],
             "    } else if (mt_has_next) {",
             "        const unsigned tile_m0 = mt_next_m0;",
             "        const unsigned tile_n0 = mt_next_n0;",
             f"        const unsigned k_chunk = mt_next_kb * {tk}u;",
-            *[f"        {ld.render_fetch()}" for ld in loads],
+            *[f"        {ld.render_fetch(stage='cur ^ 1u')}" for ld in loads],
             "    }",
             *[f"    {c.render_stage('cur')}" for c in computes],
-            "    if (more || mt_has_next) {",
-            *[f"        {ld.render_commit('cur ^ 1u')}" for ld in loads],
-            "    }",
-            "    __syncthreads();",
+            *_guarded("    if (more || mt_has_next) {",
+                      [f"        {c}" for c in _nonempty(ld.render_commit("cur ^ 1u") for ld in loads)]),
+            *[f"    {x}" for x in sync],
             "    mt_stage ^= 1u;",
             "}",
         ]
@@ -451,6 +467,15 @@ class MatmulMainloopFragment:
     @property
     def sub_fragments(self) -> tuple[KernelFragment, ...]:
         return self.fragments
+
+
+def _nonempty(lines) -> list[str]:
+    return [x for x in lines if x]
+
+
+def _guarded(head: str, lines: list[str]) -> list[str]:
+    """``head`` ... ``}`` around ``lines``, or nothing when there are none."""
+    return [head, *lines, "    }"] if lines else []
 
 
 def _epilogue_lines(t: TileConfig, out: str, value: str, check: bool, M: str, N: str) -> str:

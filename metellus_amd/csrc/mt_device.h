@@ -22,6 +22,9 @@
 //   * MT_GLOBAL               global address space qualifier (pointer tables
 //                             of batched kernels hold global pointers, which
 //                             keeps their loads global_load, not flat_load)
+//   * mt_tile_dma / mt_swz    direct-to-LDS tile loads (global_load_lds_dwordx4,
+//                             no registers, no LDS stores) into dense tiles
+//                             whose 16-byte slots are XOR-swizzled per row
 //   * mt_mfma_tile            fp32 MFMA (v_mfma_f32_32x32x2f32) over one LDS
 //                             k-chunk for a wave's WM x WN grid of 32x32 blocks
 //   * mt_acc_row              row of accumulator register v in a 32x32 block
@@ -528,6 +531,89 @@ struct mt_tile_scalar_g : mt_tile_scalar<ROWS, COLS, NT> {
     }
 };
 
+// Integer helpers callable from host code too (the CPU tests check them).
+#define MT_HD __host__ __device__ __forceinline__
+
+// ---------------------------------------------------------------------------
+// Direct-to-LDS tile loads (gfx950 global_load_lds_dwordx4).  One such load
+// moves 16 bytes per lane from global memory straight into LDS at
+// M0 + 16 * lane, so a wave writes 1 KiB of contiguous LDS per instruction
+// and no registers or LDS-store instructions are spent on the tile.  Tiles
+// are therefore dense; operand tiles the MFMAs read row-wise with 128-bit
+// reads permute the 16-byte slots of each row by mt_swz (an XOR of the
+// slot index), which keeps those reads free of bank conflicts.
+//
+// The loads are issued from inline asm: the compiler then does not see an
+// LDS write it would wait for before every later LDS read (it cannot tell
+// the stage being filled from the one being read).  The mainloop waits for
+// them itself (s_waitcnt) before the barrier that publishes the chunk.
+// ---------------------------------------------------------------------------
+
+// Physical slot permutation of row r of a dense LDS tile with S 16-byte slots
+// per row (slot p holds logical slot p ^ mt_swz<S>(r)).  It depends on
+// r mod 16 only, and makes the slots read by 8 consecutive rows, and by the
+// even and the odd rows among 16 consecutive ones, pairwise distinct -- a
+// 128-bit read of one slot per row by consecutive lanes then meets no bank
+// conflict whether the LDS serves 128 or 256 bytes per cycle.
+template <int S>
+MT_HD unsigned mt_swz(unsigned r) {
+    static_assert(S == 4 || S == 8, "swizzle defined for 16- and 32-float rows");
+    if constexpr (S == 8) return ((r >> 1) ^ ((r & 1u) << 2)) & 7u;
+    return ((r >> 1) ^ (r >> 2)) & 3u;
+}
+
+MT_INLINE unsigned mt_lds_addr(const float* p) {
+    return (unsigned)(unsigned long long)(const __attribute__((address_space(3))) float*)p;
+}
+
+// 16 bytes from g to LDS byte address lds_byte + 16 * lane (lds_byte wave
+// uniform).  One wait state separates the M0 write from the load reading it.
+MT_INLINE void mt_dma16(const float* g, unsigned lds_byte) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(g), "s"(lds_byte)
+                 : "memory", "m0");
+}
+
+// Where a direct-to-LDS load puts its data: lane `lane` of wave-load `inst`
+// writes physical slot 64 inst + lane of a dense tile with S slots per row,
+// i.e. row r, physical slot p; it loads the row's logical slot p (SWZ: p ^
+// mt_swz<S>(r)), so logical slot L of row r sits at physical L ^ mt_swz<S>(r).
+template <int S, bool SWZ>
+MT_HD void mt_dma_slot(unsigned inst, unsigned lane, unsigned& r, unsigned& logical) {
+    const unsigned slot = inst * 64u + lane;
+    r = slot / S;
+    logical = slot % S;
+    if constexpr (SWZ) logical ^= mt_swz<S>(r);
+}
+
+// ROWS x COLS tile of a row-major source (row stride rs floats, a multiple of
+// 4; 16-byte aligned base) at (row0, col0), every element in bounds, into a
+// dense LDS tile; SWZ permutes each row's slots by mt_swz.  Wave w issues
+// wave-loads w PERW .. w PERW + PERW - 1, each 1 KiB of contiguous LDS.
+template <int ROWS, int COLS, int NT, bool SWZ>
+struct mt_tile_dma {
+    static constexpr int S = COLS / 4;
+    static constexpr int INSTR = ROWS * S / 64;
+    static constexpr int PERW = INSTR / (NT / 64);
+    static_assert(COLS % 4 == 0 && (ROWS * S) % 64 == 0 && INSTR % (NT / 64) == 0,
+                  "the tile must split into whole 1 KiB wave loads, the same number per wave");
+
+    MT_INLINE void fetch(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
+                         float* lds, unsigned tid) const {
+        const unsigned lane = tid & 63u;
+        const unsigned wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const unsigned base = __builtin_amdgcn_readfirstlane(mt_lds_addr(lds));
+#pragma unroll
+        for (int q = 0; q < PERW; ++q) {
+            const unsigned inst = wave * PERW + q;
+            unsigned r, logical;
+            mt_dma_slot<S, SWZ>(inst, lane, r, logical);
+            mt_dma16(src + (size_t)(row0 + r) * rs + col0 + 4u * logical, base + inst * 1024u);
+        }
+    }
+};
+
 // ---------------------------------------------------------------------------
 // fp32 MFMA over one LDS k-chunk.
 //
@@ -541,18 +627,30 @@ struct mt_tile_scalar_g : mt_tile_scalar<ROWS, COLS, NT> {
 // As points at the wave's first A row in an LDS tile [rows][LDA] (row-major,
 // m x k); Bs at the wave's first column in an LDS tile [TK][LDB] (k x n).
 // acc[i][j] is the 32x32 block at rows 32*i, cols 32*j of the wave tile.
+//
+// Layouts: A rows of LDA floats, or (ASWZ) a dense [rows][TK] tile written by
+// direct-to-LDS loads whose 16-byte slots are permuted by mt_swz; B either
+// [TK][LDB] (k-major), or (BNM) n-major [cols][TK] swizzled like A and read
+// 128 bits at a time.  Every layout feeds the MFMAs the same values in the
+// same order, so results are identical across layouts.
 // ---------------------------------------------------------------------------
 
-template <int WM, int WN, int TK, int LDA, int LDB>
+template <int WM, int WN, int TK, int LDA, int LDB, bool ASWZ = false, bool BNM = false>
 MT_INLINE void mt_mfma_tile(const float* __restrict__ As, const float* __restrict__ Bs,
                             mt_f32x16 (&acc)[WM][WN], unsigned lane) {
     static_assert(TK % 8 == 0, "TK must be a multiple of 8");
     static_assert(LDA % 4 == 0, "LDA must keep 16-byte alignment");
+    static_assert(!ASWZ || LDA == TK, "a swizzled A tile is dense");
+    static_assert(!BNM || LDB == TK, "an n-major B tile is dense");
     constexpr int HALF = TK / 2;
     const unsigned li = lane & 31u;
     const unsigned lh = lane >> 5;
-    const float* a_base = As + li * LDA + lh * HALF;
-    const float* b_base = Bs + (lh * HALF) * LDB + li;
+    // Swizzled tiles: the wave's first row is a multiple of 16, so row
+    // 32 i + li of the wave permutes its slots by mt_swz(li).
+    unsigned m = 0u;
+    if constexpr (ASWZ || BNM) m = mt_swz<TK / 4>(li);
+    const float* a_base = ASWZ ? As + li * TK : As + li * LDA + lh * HALF;
+    const float* b_base = BNM ? Bs + li * TK : Bs + (lh * HALF) * LDB + li;
     // Raise this wave's issue priority while it feeds the matrix core, so a
     // wave still holding MFMAs is preferred over one writing the next chunk
     // to LDS or waiting at the barrier (measured +2.6-3.6 % on 4096^3 and
@@ -560,14 +658,21 @@ MT_INLINE void mt_mfma_tile(const float* __restrict__ As, const float* __restric
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s0 = 0; s0 < HALF; s0 += 4) {
+        const unsigned slot = (lh * HALF + (unsigned)s0) / 4u;  // swizzled tiles: logical 16-byte slot
         mt_f32x4 a[WM];
 #pragma unroll
-        for (int i = 0; i < WM; ++i) a[i] = mt_ld4(a_base + i * 32 * LDA + s0);
+        for (int i = 0; i < WM; ++i)
+            a[i] = ASWZ ? mt_ld4(a_base + i * 32 * TK + 4u * (slot ^ m)) : mt_ld4(a_base + i * 32 * LDA + s0);
+        mt_f32x4 bv[BNM ? WN : 1];
+        if constexpr (BNM) {
+#pragma unroll
+            for (int j = 0; j < WN; ++j) bv[j] = mt_ld4(b_base + j * 32 * TK + 4u * (slot ^ m));
+        }
 #pragma unroll
         for (int ss = 0; ss < 4; ++ss) {
             float b[WN];
 #pragma unroll
-            for (int j = 0; j < WN; ++j) b[j] = b_base[(s0 + ss) * LDB + j * 32];
+            for (int j = 0; j < WN; ++j) b[j] = BNM ? bv[j][ss] : b_base[(s0 + ss) * LDB + j * 32];
 #pragma unroll
             for (int i = 0; i < WM; ++i) {
 #pragma unroll
@@ -619,7 +724,6 @@ MT_INLINE void mt_zero(mt_f32x16& a) {
 #define MT_SK_SPIN_LIMIT (1u << 22)
 // The schedule is plain integer arithmetic, callable from host code too (the
 // CPU test suite checks its coverage and wait order).
-#define MT_HD __host__ __device__ __forceinline__
 
 struct mt_stream_k {
     unsigned chunks, P, w, j, dp, sk0, nsk, ndp;

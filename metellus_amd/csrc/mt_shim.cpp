@@ -217,30 +217,52 @@ void mkdirs(const std::string& path) {
     }
 }
 
-bool disk_load(const std::string& file, std::vector<char>* code) {
+// A cache file holds the 8-byte length of its key, the key itself, then the
+// code object.  The file name is only a hash of the key: a load compares the
+// stored key with the wanted one, so a hash collision or a truncated file is
+// a miss, never a wrong kernel.
+bool disk_load(const std::string& file, const std::string& key, std::vector<char>* code) {
     FILE* f = std::fopen(file.c_str(), "rb");
     if (!f) return false;
     std::fseek(f, 0, SEEK_END);
-    long n = std::ftell(f);
+    const long n = std::ftell(f);
     std::fseek(f, 0, SEEK_SET);
-    bool ok = n > 0;
+    uint64_t klen = 0;
+    bool ok = n > 8 && std::fread(&klen, sizeof(klen), 1, f) == 1 && klen == key.size() &&
+              static_cast<uint64_t>(n) > 8 + klen;
     if (ok) {
-        code->resize(static_cast<size_t>(n));
+        std::string stored(klen, '\0');
+        ok = std::fread(&stored[0], 1, klen, f) == klen && stored == key;
+    }
+    if (ok) {
+        code->resize(static_cast<size_t>(n) - 8 - klen);
         ok = std::fread(code->data(), 1, code->size(), f) == code->size();
     }
     std::fclose(f);
     return ok;
 }
 
-void disk_store(const std::string& dir, const std::string& file, const std::vector<char>& code) {
+void disk_store(const std::string& dir, const std::string& file, const std::string& key,
+                const std::vector<char>& code) {
     mkdirs(dir);
     std::string tmp = file + ".tmp" + std::to_string(static_cast<long>(getpid()));
     FILE* f = std::fopen(tmp.c_str(), "wb");
     if (!f) return;
-    bool ok = std::fwrite(code.data(), 1, code.size(), f) == code.size();
-    std::fclose(f);
+    const uint64_t klen = key.size();
+    bool ok = std::fwrite(&klen, sizeof(klen), 1, f) == 1 &&
+              std::fwrite(key.data(), 1, key.size(), f) == key.size() &&
+              std::fwrite(code.data(), 1, code.size(), f) == code.size();
+    ok = (std::fclose(f) == 0) && ok;
     if (ok) std::rename(tmp.c_str(), file.c_str());
     else std::remove(tmp.c_str());
+}
+
+// The compiler's version is part of every cache key, so code objects built
+// by another hiprtc are never reused.
+std::string compiler_tag() {
+    int major = 0, minor = 0;
+    if (hiprtcVersion(&major, &minor) != HIPRTC_SUCCESS) return "hiprtc-unknown";
+    return "hiprtc-" + std::to_string(major) + "." + std::to_string(minor);
 }
 
 }  // namespace
@@ -424,6 +446,8 @@ int mt_compile(const char* source, const char* function_name, const char* option
     key.append(source).push_back('\0');
     key.append(function_name).push_back('\0');
     for (auto& o : opts) key.append(o).push_back(' ');
+    static const std::string tag = compiler_tag();
+    key.append(tag);
     auto hit = s.by_key.find(key);
     if (hit != s.by_key.end()) {
         ++s.hits;
@@ -435,12 +459,12 @@ int mt_compile(const char* source, const char* function_name, const char* option
     char name[32];
     std::snprintf(name, sizeof(name), "%016llx.co", static_cast<unsigned long long>(fnv1a(key)));
     std::string file = dir.empty() ? "" : dir + "/" + name;
-    if (!file.empty() && disk_load(file, &code)) {
+    if (!file.empty() && disk_load(file, key, &code)) {
         ++s.hits;
     } else {
         if (rtc_compile(source, opts, &code)) return 1;
         ++s.compiled;
-        if (!file.empty()) disk_store(dir, file, code);
+        if (!file.empty()) disk_store(dir, file, key, code);
     }
     Kernel k{};
     MT_HIP(hipModuleLoadData(&k.module, code.data()));

@@ -79,7 +79,7 @@ class TgLoadFragment:
     # gfx950 layout controls
     dst_pitch: int | None = None
     stages: int = 1
-    mode: str | None = None  # "colvec" | "rowvec" | "scalar" (default: from strides)
+    mode: str | None = None  # "colvec" | "rowvec" | "scalar" | "dma" (default: from strides)
     transform_lambda: str | None = None
     # Apply the transform when the registers are written to LDS rather than
     # when the loads return, so a pipelined mainloop does not wait for the
@@ -96,6 +96,13 @@ class TgLoadFragment:
     # column broadcast for "colvec", a row broadcast for "rowvec"): gather
     # them once per 128-bit slot.
     gather_per_slot: bool = False
+    # mode "dma": direct-to-LDS loads (mt_tile_dma) of a row-major source
+    # (row stride src_row_stride, unit column stride, every element in
+    # bounds, no transform) into a dense tile of tile_shape; the fetch
+    # writes LDS stage ``stage`` itself and there is no commit.  The
+    # consumer waits for the loads (s_waitcnt) before its barrier.
+    # ``dma_swizzle`` permutes each row's 16-byte slots (mt_swz).
+    dma_swizzle: bool = False
 
     @property
     def pitch(self) -> str:
@@ -142,9 +149,27 @@ class TgLoadFragment:
     def gathering(self) -> bool:
         return self.gather_lambda is not None
 
+    @property
+    def is_dma(self) -> bool:
+        return self.mode == "dma"
+
+    def _check_dma(self) -> None:
+        rows, cols = self.tile_shape
+        if self.check or self._has_transform() or self.gathering or self.src_col_stride != "1":
+            raise ValueError(f"{self.name}: direct-to-LDS loads need an unmasked, untransformed row-major source")
+        if self.stages < 2 or (self.dst_pitch is not None and self.dst_pitch != cols):
+            raise ValueError(f"{self.name}: direct-to-LDS loads fill a dense, double-buffered tile")
+        slots = rows * cols // 4
+        if cols % 4 or slots % 64 or (slots // 64) % (self.num_threads // 64):
+            raise ValueError(f"{self.name}: a {rows}x{cols} tile does not split into whole wave loads")
+
     def render_decl(self) -> str:
         rows, cols = self.tile_shape
         mode = self.resolved_mode()
+        if mode == "dma":
+            self._check_dma()
+            swz = "true" if self.dma_swizzle else "false"
+            return f"const mt_tile_dma<{rows}, {cols}, {self.num_threads}, {swz}> {self.loader};"
         tmpl = {"colvec": "mt_tile_colvec", "colvec_safe": "mt_tile_colvec", "rowvec": "mt_tile_rowvec",
                 "scalar": "mt_tile_scalar"}[mode]
         if self.gathering:
@@ -160,7 +185,16 @@ class TgLoadFragment:
             )
         return f"{tmpl}<{rows}, {cols}, {self.num_threads}> {self.loader};\nconst auto {self.xform} = {self._lambda()};"
 
-    def render_fetch(self, tid: str = "threadIdx.x") -> str:
+    def render_fetch(self, tid: str = "threadIdx.x", stage: str | None = None) -> str:
+        """The loads of one tile; ``stage`` is the LDS buffer a direct-to-LDS
+        loader writes (register loaders write at commit and ignore it)."""
+        if self.is_dma:
+            if stage is None:
+                raise ValueError(f"{self.name}: a direct-to-LDS fetch needs its LDS stage")
+            return (
+                f"{self.loader}.fetch({self.src_name}, {self.src_row_stride}, {self.row_start}, "
+                f"{self.col_start}, {self.stage_ptr(stage)}, {tid});"
+            )
         rlim = self.row_limit if self.row_limit is not None else "0xffffffffu"
         clim = self.col_limit if self.col_limit is not None else "0xffffffffu"
         check = "true" if self.check else "false"
@@ -195,6 +229,8 @@ class TgLoadFragment:
         return f"&{self.dst_name}[0][0]"
 
     def render_commit(self, stage: str = "0", tid: str = "threadIdx.x") -> str:
+        if self.is_dma:
+            return ""
         if self.gathering:
             check = "true" if self.check else "false"
             return (
@@ -211,7 +247,11 @@ class TgLoadFragment:
 
     def render(self, ctx: CodegenContext) -> str:
         tid = flat_tid(ctx)
-        return "{\n" + "\n".join([self.render_decl(), self.render_fetch(tid), self.render_commit("0", tid)]) + "\n}"
+        if self.is_dma:
+            body = [self.render_decl(), self.render_fetch(tid, "0"), "__builtin_amdgcn_s_waitcnt(0);"]
+        else:
+            body = [self.render_decl(), self.render_fetch(tid), self.render_commit("0", tid)]
+        return "{\n" + "\n".join(body) + "\n}"
 
     @property
     def lds_shape(self) -> tuple[int, ...]:

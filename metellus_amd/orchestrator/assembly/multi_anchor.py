@@ -43,7 +43,7 @@ from metellus_amd.orchestrator.assembly.decision import DecisionView
 from metellus_amd.orchestrator.assembly.expressions import ChainCode
 from metellus_amd.orchestrator.assembly.extras import Extras, input_param, output_param, param_name
 from metellus_amd.orchestrator.assembly import matmul as _mm
-from metellus_amd.orchestrator.assembly.matmul import b_tile_for, operand_load
+from metellus_amd.orchestrator.assembly.matmul import b_tile_for, dma_layouts, operand_load
 from metellus_amd.orchestrator.ir import Tensor
 from metellus_amd.orchestrator.kernel_group import KernelGroup
 from metellus_amd.runtime.program import Kernel
@@ -95,6 +95,8 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
     helpers.append(merge_code.helper())
     value_expr = merge_code.call(["{a0}", "{a1}"], [])
 
+    if shared:
+        tile = dma_layouts(tile, (src_a[0],), src_b, (tf_a[0],), tf_b, aligned)
     kvars = ("K", "K") if shared else ("K0", "K1")
     ks = (K0, K1)
     configs = tuple(

@@ -21,7 +21,7 @@ def test_broadcast_only_prologue_gathers_and_applies_at_commit():
     assert "mt_tile_colvec_g<" in src and "ld_A_tile.template fetch_gather<false>(" in src
     assert "ld_A_tile.template commit_apply<" in src
     assert "mt_div_fast(" in src.split('extern "C"')[0].split("prologue_a")[-1]
-    assert "ld_B_tile.template fetch<false>(" in src  # no transform on V
+    assert "ld_B_tile.fetch(g_V, " in src  # no transform on V: loaded straight into LDS
     assert ", 32, " in src.split("mt_mfma_tile<")[-1].split(">")[0] + ", "
 
 
@@ -31,14 +31,27 @@ def test_elementwise_division_stays_ieee():
     assert "mt_div_fast(" not in "".join(g.kernel.ctx.helpers)
 
 
-def test_full_operand_prologue_gathers_with_the_tile():
+def _mfma_tile_k(body: str) -> int:
+    return int(body.split("mt_mfma_tile<")[1].split(">")[0].split(",")[2])
+
+
+def test_full_operand_prologue_gathers_with_the_tile(monkeypatch):
     # (h1 * s * h2) @ W3: s and h2 are full matrices, loaded with the A tile
-    # and multiplied in when the chunk is committed; k-chunks of 16
+    # and multiplied in when the chunk is committed.  W3 goes straight to LDS,
+    # which leaves the registers for 32-wide k-chunks; with W3 loaded through
+    # registers too, the chunks are 16 wide.
+    from metellus_amd.orchestrator.assembly import matmul as am
+
     g = _by_name(compile_program(gpu_cases.mlp_block(128, 128, 384)))["matmul_out_fused"]
     body = g.kernel.source.split('extern "C"')[1]
     assert "mt_tile_colvec_g<" in body and ", 2> ld_A_tile;" in body
     assert "ld_A_tile.template fetch_gather<" in body and "ld_A_tile.template commit_apply<" in body
-    assert "mt_mfma_tile<" in body and ", 16, " in body.split("mt_mfma_tile<")[1].split(">")[0] + ", "
+    assert "ld_B_tile.fetch(g_W3, " in body and _mfma_tile_k(body) == 32
+    assert hip_backend.compile_only(g.kernel.source) > 0
+    monkeypatch.setattr(am, "DMA_LOADS", False)
+    g = _by_name(compile_program(gpu_cases.mlp_block(128, 128, 384)))["matmul_out_fused"]
+    body = g.kernel.source.split('extern "C"')[1]
+    assert "mt_tile_dma<" not in body and _mfma_tile_k(body) == 16
     assert hip_backend.compile_only(g.kernel.source) > 0
 
 

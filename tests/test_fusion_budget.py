@@ -1,11 +1,13 @@
 """The LDS budget gate of ``fuse`` (the reference's
 tests/test_fusion_budget.py, re-derived for gfx950 tiles).
 
-gfx950 numbers used below (64x64x32 MFMA tile for 64x64 operands, A rows
-padded to 36 floats and B rows to 68, double-buffered): one matmul = A
-2x64x36 + B 2x32x68 floats = 35,840 B; the diamond (shared A, two B chunks)
-= 53,248 B; the non-shared multi-producer = 35,840 B because its second
-mainloop's tiles alias the first's.  The real cap is 163,840 B."""
+gfx950 numbers used below (64x64x32 MFMA tile for 64x64 operands,
+double-buffered).  A single matmul and the diamond load their operand tiles
+straight into dense LDS tiles: one matmul = A 2x64x32 + B 2x32x64 floats =
+32,768 B; the diamond (shared A, two B chunks) = 49,152 B.  The non-shared
+multi-producer fills registers-first tiles with padded rows (A rows of 36
+floats, B rows of 68): 35,840 B, because its second mainloop's tiles alias
+the first's.  The real cap is 163,840 B."""
 
 import pytest
 
@@ -56,14 +58,14 @@ def test_fits_under_cap_unchanged():
 def test_budget_numbers():
     (d,) = fuse(_pair(True).build())
     (m,) = fuse(_pair(False).build())
-    assert _budget(d) == 53_248
+    assert _budget(d) == 49_152
     assert _budget(m) == 35_840  # A1/B1 alias A0/B0
     ops = Operations()
     ops.input("A", shape=(64, 64))
     ops.input("B", shape=(64, 64))
     ops.matmul(a="A", b="B", out="C")
     (p,) = fuse(ops.build())
-    assert _budget(p) == 35_840
+    assert _budget(p) == 32_768
 
 
 def test_overflowing_fusion_is_blacklisted_and_split(monkeypatch):
