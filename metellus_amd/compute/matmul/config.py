@@ -132,6 +132,17 @@ SINGLE_ANCHOR_TILES = (
     TileConfig(32, 32, 32, 1, 1),
 )
 
+# 16-wave tiles (4 waves per SIMD): offered when the operand chunks leave the
+# registers for it (no full-size gathered prologue operands) -- measured on
+# MI355X with direct-to-LDS loads: 4096^3 977.7 -> 968.0 us (2x8 waves of
+# 128x32), C4 X @ W1 2650 -> 2609 us, C5 S 287.2 -> 283.6 us, C5 P @ V
+# 280.3 -> 274.2 us (256x128 as 4x4 waves of 64x32).  4x4 waves of 64x64 on
+# 256x256 were slower than 2x8 (987 us).
+WIDE_TILES = (
+    TileConfig(256, 256, 32, 2, 8),
+    TileConfig(256, 128, 32, 4, 4),
+)
+
 DUAL_ANCHOR_TILES = (
     TileConfig(256, 128, 32, 4, 2),
     TileConfig(128, 128, 32, 2, 2),
@@ -224,20 +235,23 @@ def uses_stream_k(M: int, K: int, N: int, t: TileConfig, workgroups: int | None,
     return rem != 0 and rem * ceil_div(K, t.tile_K) >= workgroups
 
 
-def select_tile_config(M: int, K: int, N: int, anchors: int = 1, batch: int = 1) -> TileConfig:
+def select_tile_config(
+    M: int, K: int, N: int, anchors: int = 1, batch: int = 1, wide: bool = False
+) -> TileConfig:
     """Highest ``tile_score``; ties go to more resident waves, then more
     workgroups.  ``batch``
     identical problems launched together (grid z) count toward filling the
     GPU.  Tiles wider than the (power-of-two rounded) output are skipped.
-    Measured on MI355X: 256x256 (8 waves) for 4096^3 and the C4/C5 Q.K^T
-    GEMMs; 128x128 (8 waves) for the C5 P.V GEMM (N = 128, batched heads)."""
+    ``wide`` adds the 16-wave tiles (single anchor only).
+    Measured on MI355X: 256x256 for 4096^3 and the C4/C5 Q.K^T GEMMs
+    (16 waves when wide, else 8); 256x128 as 16 waves (wide) or 128x128 as
+    8 waves for the C5 P.V GEMM (N = 128, batched heads)."""
     if FORCE_TILE is not None:
         return FORCE_TILE
-    cands = [
-        t
-        for t in (SINGLE_ANCHOR_TILES if anchors == 1 else DUAL_ANCHOR_TILES)
-        if t.tile_M <= _pow2_at_least(M) and t.tile_N <= _pow2_at_least(N)
-    ]
+    pool = SINGLE_ANCHOR_TILES if anchors == 1 else DUAL_ANCHOR_TILES
+    if wide and anchors == 1:
+        pool = WIDE_TILES + pool
+    cands = [t for t in pool if t.tile_M <= _pow2_at_least(M) and t.tile_N <= _pow2_at_least(N)]
     best = None
     best_key = None
     for i, t in enumerate(cands):

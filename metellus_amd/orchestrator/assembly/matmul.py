@@ -184,6 +184,11 @@ def dma_layouts(tile: TileConfig, srcs_a, srcs_b, pros_a, pros_b, aligned: bool)
     return dataclasses.replace(tile, a_layout="swz" if a_ok else "pad", b_layout=b_layout)
 
 
+# 16-wave tiles (config.WIDE_TILES) for matmuls whose prologues gather no
+# full-size operands and whose shape needs no bounds checks.
+WIDE_TILES = True
+
+
 def gathers(prologue: ChainCode | None) -> bool:
     return GATHER_PROLOGUES and prologue is not None and len(prologue.externals) > 0
 
@@ -213,8 +218,6 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
     assert isinstance(src_a, Tensor) and isinstance(src_b, Tensor)
     M, K = anchor.a.shape
     N = anchor.b.shape[1]
-    tile = b_tile_for(select_tile_config(M, K, N, batch=batch), src_b, K, N)
-    aligned = is_aligned_shape(M, K, N, tile)
     final_out = decision.epilogue[-1].out if decision.epilogue else anchor.out
     out_key = final_out.buffer_key
 
@@ -242,8 +245,16 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         helpers.append(epi.helper())
         value_expr = epi.scalar_call(["{a0}"], "row", "col")
 
+    full_gather = gathers_full_operands(pro_a) or gathers_full_operands(pro_b)
+    tile = b_tile_for(select_tile_config(M, K, N, batch=batch, wide=WIDE_TILES and not full_gather), src_b, K, N)
+    aligned = is_aligned_shape(M, K, N, tile)
+    if tile.num_threads > 512 and not aligned:
+        # 16-wave tiles only without bounds checks (their masks cost registers)
+        tile = b_tile_for(select_tile_config(M, K, N, batch=batch), src_b, K, N)
+        aligned = is_aligned_shape(M, K, N, tile)
+
     tile = dma_layouts(tile, (src_a,), (src_b,), (pro_a,), (pro_b,), aligned)
-    if (gathers_full_operands(pro_a) or gathers_full_operands(pro_b)) and tile.b_layout == "pad":
+    if full_gather and tile.b_layout == "pad":
         # a B chunk loaded through registers leaves no room for full-size
         # gathered operands at 32-wide chunks; a directly loaded B does
         # (measured, C4 (h1*s*h2) @ W3: 2.93 ms with 16-wide chunks, 2.89 ms

@@ -128,9 +128,10 @@ def test_c4_literal_four_kernels():
     assert gs[3].bindings == ("h1", "W3", "out", "s", "h2")
     assert gs[3].dims == (4096, 11008, 4096)
     # 256x256 tiles: 43 x 16 = 688 tiles > 256 resident workgroups, so the
-    # GEMM runs as 256 persistent workgroups; X @ W3 has exactly 256 tiles
-    assert gs[0].grid == (256, 1, 1) and gs[0].threads == (512, 1, 1)
-    assert gs[3].grid == (16, 16, 1)
+    # GEMM runs as 256 persistent workgroups of 16 waves; X @ W3 (its
+    # prologue gathers the full-size s and h2) has exactly 256 tiles, 8 waves
+    assert gs[0].grid == (256, 1, 1) and gs[0].threads == (1024, 1, 1)
+    assert gs[3].grid == (16, 16, 1) and gs[3].threads == (512, 1, 1)
 
 
 def test_c4_diamond_fuses_under_160k():
