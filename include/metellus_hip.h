@@ -55,11 +55,14 @@ int mt_device_ptr(uint64_t handle, uint64_t* address);
 
 /* write_buffer (reference: src/metal_backend.mm:110-117): copies nbytes from
  * host memory; nbytes must not exceed the buffer size.  Returns after the
- * copy completed. */
+ * copy completed.  Copies of >= 4 MiB from pageable memory go through the
+ * shim's page-locked staging ring (parallel host copies overlapped with the
+ * DMA); page-locked sources are copied directly. */
 int mt_write(uint64_t handle, const void* src, size_t nbytes);
 
 /* read_buffer (reference: src/metal_backend.mm:119-126): waits for all
- * queued work, then copies nbytes to host memory. */
+ * queued work, then copies nbytes to host memory (staged like mt_write when
+ * the destination is pageable and nbytes >= 4 MiB). */
 int mt_read(uint64_t handle, void* dst, size_t nbytes);
 
 /* fill_buffer (reference: src/metal_backend.mm:128-141): byte fill. */
