@@ -6,11 +6,16 @@ src/compute/matmul/config.py:40-51: 32x32x16 .. 128x64x32 tiles, four
 ``tile_M x tile_N`` output tile with fp32 MFMA (32x32 blocks); each wave owns
 a ``(tile_M/sg_M) x (tile_N/sg_N)`` sub-tile, i.e. ``WM x WN`` accumulator
 blocks of 16 registers.  A and B k-chunks of ``tile_K`` are double-buffered
-in LDS (rows padded by ``a_pad``/``b_pad`` floats to spread LDS banks).
+in LDS: dense, XOR-swizzled tiles filled by direct-to-LDS loads, or rows
+padded by ``a_pad``/``b_pad`` floats when filled through registers (see
+``TileConfig.a_layout`` / ``b_layout``).
 
-``select_tile_config`` takes the largest tile that still yields at least one
-workgroup per compute unit (256 on MI355X); shapes too small for that get the
-tile giving the most workgroups.
+``select_tile_config`` scores each candidate by tile area x resident waves per
+SIMD x useful fraction x grid fill (``tile_score``) and takes the best; the
+16-wave tiles are candidates only when the caller says the operands leave the
+registers for them (``wide``).  Large problems then run as persistent
+workgroups (``persistent_workgroups``) with a stream-K last round
+(``uses_stream_k``).
 """
 
 from __future__ import annotations
