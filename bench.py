@@ -20,7 +20,7 @@ heads, ``api.run_batch``), each kernel against its roofline.
 ``cpu_baseline``: the CPU oracle (NumPy, single-threaded ufuncs) evaluating
 the same C2 expression on the same full-size inputs for ~10 s on the host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|fragments]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|fragments|ceilings]
        [--no-extra] [--no-cpu] [--no-flush] [--calibrate-copy]
 """
 
@@ -445,6 +445,40 @@ def cpu_baseline_config(label: str, made, per_kernel: list[dict], budget_s: floa
     }
 
 
+def ceiling_benches(steps: int, flusher) -> list[dict]:
+    """HBM ceilings of C2's access pattern through this framework's own
+    kernels with trivial arithmetic: 4 reads + 1 write of 64 MiB each (C2's
+    bytes, adds instead of the sigmoid chain), 1 read + 1 write (a copy),
+    and reads only (a row sum of 256 MiB).  C2 at the 4-read-1-write figure
+    means its chain costs nothing and the kernel is at the pattern's HBM
+    limit on this box."""
+    from metellus_amd.orchestrator import Operations
+
+    rng = np.random.default_rng(7)
+    mk = lambda shape: rng.standard_normal(shape).astype(np.float32)
+    out = []
+    ops = Operations()
+    for n in "abcd":
+        ops.from_numpy(mk((4096, 4096)), n)
+    ops.elementwise("add", out="t1", operands=("a", "b"))
+    ops.elementwise("add", out="t2", operands=("t1", "c"))
+    ops.elementwise("add", out="sum4", operands=("t2", "d"))
+    cases = [("ceiling: 4 reads + 1 write, 64 MiB each", ops)]
+    ops = Operations()
+    ops.from_numpy(mk((4096, 4096)), "x")
+    ops.elementwise("mul", out="copy", operands=("x", 1.0))
+    cases.append(("ceiling: 1 read + 1 write, 64 MiB each", ops))
+    ops = Operations()
+    ops.from_numpy(mk((8192, 8192)), "x")
+    ops.reduction("sum", out="rows", x="x")
+    cases.append(("ceiling: read 256 MiB (row sums)", ops))
+    for label, ops in cases:
+        prep = Prepared(ops)
+        out += time_kernels(prep, steps, 2, flusher, label)
+        prep.release()
+    return out
+
+
 def fragment_benches(steps: int, flusher) -> list[dict]:
     """The reference's fragment-level benches (tests/bench_init.py,
     bench_reduction.py, bench_elementwise.py, bench_matmul.py) at their own
@@ -668,6 +702,8 @@ def main() -> int:
 
     if only == "fragments":
         per_config += fragment_benches(max(3, min(args.steps, 10)), flush)
+    if only == "ceilings":
+        per_config += ceiling_benches(max(3, args.steps), flush)
 
     # ---- other configs -----------------------------------------------------
     if (not args.no_extra and only is None) or only not in (None, "c2", "fragments"):
