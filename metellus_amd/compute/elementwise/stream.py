@@ -36,15 +36,19 @@ NWAVES = 4
 NT = 64 * NWAVES
 
 # Streaming policy, chosen by measurement on MI355X with the Infinity Cache
-# flushed (C2 chain 4096^2, C3 chains 8192^2): nontemporal 128-bit loads,
-# ordinary stores; flat: 1024 lanes x 1 float4 per lane (~6.1 TB/s; the
-# 256-1024 lane, 1-4 float4 variants all land within 5.9-6.1 TB/s); tiled:
-# 8 elements per lane (~6.8 TB/s).
+# flushed (C2 chain 4096^2, C3 chains 8192^2): nontemporal 128-bit loads;
+# 128-bit stores at device scope (sc1), which on gfx950 write through the
+# XCD's L2 instead of leaving dirty lines there (same-process A/B: C2 53.57 ->
+# 51.67 us, C3 chains, C4 sigmoid and C5 e chains +2.7-3.5 %; nontemporal
+# stores were 4 % slower than ordinary ones); flat: 1024 lanes x 1 float4 per
+# lane (the 256-1024 lane, 1-4 float4 variants all land within 3 %); tiled:
+# 8 elements per lane.
 FLAT_THREADS = 1024
 FLAT_UNROLL = 1
 TILED_ELEMS = 8  # elements per lane in the tiled layout
 NT_LOAD = True
 NT_STORE = False
+WT_STORE = True
 
 
 def _ceil_div(a: int, b: int) -> int:
@@ -67,6 +71,7 @@ class StreamLayout:
     threads: int = NT  # lanes per workgroup (flat layout)
     nt_load: bool = NT_LOAD  # nontemporal (streaming) loads
     nt_store: bool = NT_STORE  # nontemporal stores
+    wt_store: bool = WT_STORE  # device-scope stores (write through L2); wins over nt_store
 
     def tile(self) -> tuple[int, int]:
         """(TM, TN) of one workgroup for the tiled layout."""
@@ -85,13 +90,14 @@ def choose_layout(primary: Tensor, externals: list[External], M: int, N: int) ->
     if flat:
         assert FLAT_THREADS % 64 == 0 and FLAT_THREADS <= 1024
         return StreamLayout(
-            "flat", vec=4, unroll=FLAT_UNROLL, threads=FLAT_THREADS, nt_load=NT_LOAD, nt_store=NT_STORE
+            "flat", vec=4, unroll=FLAT_UNROLL, threads=FLAT_THREADS, nt_load=NT_LOAD, nt_store=NT_STORE,
+            wt_store=WT_STORE,
         )
     vec = 4 if N % 4 == 0 else 1
     lpr = min(64, _next_pow2(_ceil_div(N, vec)))
     rows_per_step = NWAVES * (64 // lpr)
     rpw = max(1, min(max(1, TILED_ELEMS // vec), _ceil_div(M, rows_per_step)))
-    return StreamLayout("tiled", vec=vec, unroll=rpw, lpr=lpr, nt_load=NT_LOAD, nt_store=NT_STORE)
+    return StreamLayout("tiled", vec=vec, unroll=rpw, lpr=lpr, nt_load=NT_LOAD, nt_store=NT_STORE, wt_store=WT_STORE)
 
 
 def grid_for_layout(layout: StreamLayout, M: int, N: int) -> tuple[int, int, int]:
@@ -135,6 +141,8 @@ class ElementwiseStreamFragment:
         return f"mt_ld4_nt({addr})" if self.layout.nt_load else f"mt_ld4({addr})"
 
     def _st4(self, addr: str, val: str) -> str:
+        if self.layout.wt_store:
+            return f"mt_st4_wt({addr}, {val})"
         return f"mt_st4_nt({addr}, {val})" if self.layout.nt_store else f"mt_st4({addr}, {val})"
 
     def render(self, ctx: CodegenContext) -> str:

@@ -5,7 +5,8 @@
 // expressions arrive as lambdas (prologue transforms, epilogues, merges).
 //
 //   * mt_dims                 dims passed by value in the kernel arguments
-//   * mt_ld4 / mt_st4         128-bit global loads / stores
+//   * mt_ld4 / mt_st4         128-bit global loads / stores (_nt: nontemporal;
+//                             mt_st4_wt: device scope, written through L2)
 //   * mt_div_fast             division feeding a matmul (refined reciprocal
 //                             times x, within 2 ulp; IEEE division at the edges)
 //   * mt_wave_*               wave64 butterfly reductions (fixed order)
@@ -58,6 +59,12 @@ MT_INLINE mt_f32x4 mt_ld4_nt(const float* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const mt_f32x4*>(p));
 }
 MT_INLINE void mt_st4_nt(float* p, mt_f32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<mt_f32x4*>(p)); }
+// 128-bit global store at device scope (sc1): it writes through the XCD's L2
+// instead of leaving a dirty line there, which suits outputs written once by
+// streaming kernels.  p must point to global memory (never LDS).
+MT_INLINE void mt_st4_wt(float* p, mt_f32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
 
 // x / y where the quotient enters a matmul.  r is the hardware reciprocal
 // refined by one Newton step, r + r * (1 - y * r); it depends on y only, so
