@@ -18,7 +18,9 @@ attention (32 heads; each of the 5 per-head kernels launched once for all
 heads, ``api.run_batch``), each kernel against its roofline.
 
 ``cpu_baseline``: the CPU oracle (NumPy, single-threaded ufuncs) evaluating
-the same C2 expression on the same full-size inputs for ~10 s on the host.
+the same C2 expression on the same full-size inputs for ~10 s on the host;
+``per_config`` the other configurations in float32 NumPy.  ``end_to_end``:
+``api.run`` wall times for C2 and C3 (host transfers included).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|fragments|ceilings]
        [--no-extra] [--no-cpu] [--no-flush] [--calibrate-copy]
@@ -445,6 +447,28 @@ def cpu_baseline_config(label: str, made, per_kernel: list[dict], budget_s: floa
     }
 
 
+def end_to_end_runs(reps: int = 5) -> list[dict]:
+    """``api.run`` wall time (compile lookup, uploads from NumPy, kernels,
+    download of the final output) for C2 and C3 -- the reference API's
+    whole path, host transfers included; never part of ``value``."""
+    from metellus_amd.api import run
+
+    out = []
+    for label, make, outputs in (("C2", _c2, ("out",)), ("C3 softmax", _c3, ("p",))):
+        ops = make()
+        run(ops, outputs=outputs)  # compile, pools and staging buffers warm
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            run(ops, outputs=outputs)
+            ts.append(time.perf_counter() - t0)
+        up = sum(a.nbytes for a in ops.uploads.values())
+        out.append({"config": label, "run_ms_median": round(float(np.median(ts)) * 1e3, 3),
+                    "run_ms_min": round(min(ts) * 1e3, 3), "uploaded_bytes": up, "downloaded": list(outputs)})
+        log(f"[bench] run() {label}: median {np.median(ts) * 1e3:.2f} ms ({up / 2**20:.0f} MiB uploaded)")
+    return out
+
+
 def ceiling_benches(steps: int, flusher) -> list[dict]:
     """HBM ceilings of C2's access pattern through this framework's own
     kernels with trivial arithmetic: 4 reads + 1 write of 64 MiB each (C2's
@@ -735,6 +759,8 @@ def main() -> int:
     if cpu_configs:
         line.setdefault("cpu_baseline", {})["per_config"] = cpu_configs
     line["per_kernel"] = per_config
+    if only is None and not args.no_extra:
+        line["end_to_end"] = end_to_end_runs()
     print(json.dumps(line), flush=True)
     return 0
 
