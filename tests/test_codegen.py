@@ -131,3 +131,26 @@ def test_persistent_switch_off_restores_classic_grid(monkeypatch):
     monkeypatch.setattr(config, "PERSISTENT", False)
     g = compile_program(gpu_cases.plain_matmul(192, 96, 320))[0]
     assert g.grid[2] == 1 and g.grid[0] * g.grid[1] > 2
+
+
+@pytest.mark.parametrize(
+    "case",
+    [
+        lambda: gpu_cases.plain_matmul(512, 512, 512),
+        lambda: gpu_cases.attention_head(512, 128),
+        lambda: gpu_cases.mlp_block(256, 256, 512),
+    ],
+    ids=["gemm", "attention", "mlp"],
+)
+def test_direct_to_lds_kernels_wait_for_every_memory_operation(case):
+    # A direct-to-LDS chunk shares the vector-memory counter with the
+    # epilogue's stores, and the two do not retire in issue order, so the
+    # only safe wait before the barrier that publishes a chunk is a full
+    # s_waitcnt(0): a partial count can pass with the chunk still in flight.
+    dma = [g for g in compile_program(case()) if "mt_tile_dma<" in g.kernel.source.split('extern "C"')[-1]]
+    assert dma
+    for g in dma:
+        body = g.kernel.source.split('extern "C"')[-1]
+        waits = body.split("__builtin_amdgcn_s_waitcnt(")[1:]
+        assert waits, g.kernel.function_name
+        assert all(w.startswith("0)") for w in waits), g.kernel.function_name
