@@ -1,26 +1,34 @@
 """Benchmark: fused-kernel fp32 TFLOP/s and HBM GB/s (% of roofline) on 1x MI355X.
 
-Headline workload (C2): the fused elementwise
-chain ``out = sigmoid(a*b + c) * d`` on four 4096x4096 fp32 tensors (N(0,1),
-seed 1) -- one kernel, 5 x 64 MiB of algorithmic HBM traffic per step.
+Headline workload: the largest configuration, C4,
+``out = (silu(X @ W1) * (X @ W2)) @ W3`` with X 4096x4096, W1/W2 4096x11008,
+W3 11008x4096 fp32 (std 1/sqrt(fan_in), seed 3) through the fusion pipeline:
+4 kernels (X@W1, X@W2, the sigmoid chain, and (h1*s*h2)@W3 with the chain in
+the A loader), 1.108 TFLOP of matmul work per step.
 
-A *step* is one launch of the workload's fused kernel(s) on inputs already
-resident in HBM.  Before every timed step the 256 MiB Infinity Cache is
-flushed by reading a 512 MiB scratch buffer (outside the event bracket), so
-the bandwidth is HBM bandwidth.  Kernel durations come from HIP events
-recorded on the shim's stream around each launch.  Each kernel is first run
-(flush, launch) for at least 50 ms of its own GPU time, so the clocks have
-settled before the timed launches.
+A *step* is one pass of the hot path over one batch with inputs already
+resident in HBM: the workload's fused kernels launched back to back on the
+shim's stream.  Before every timed step the 256 MiB Infinity Cache is
+flushed by reading a 512 MiB scratch buffer (outside the timed bracket), so
+nothing starts cache-warm.  Timing: stream markers (HIP events without the
+system-scope fence) recorded before the first launch, between launches and
+after the last, so one step yields the step time and each kernel's time.
+Each kernel is first run (flush, launch) for at least 50 ms of its own GPU
+time, so the clocks have settled before the timed steps.  ``value`` =
+1.108 TFLOP / mean step time; ``roofline`` is the dominant kernel's (the one
+taking the largest share of the step).
 
-Also measured (``per_kernel``): C3 softmax (4 kernels), the 4096^3 matmul,
-C4 MLP block (literal 4-kernel partition and the fused diamond variant), C5
-attention (32 heads; each of the 5 per-head kernels launched once for all
-heads, ``api.run_batch``), each kernel against its roofline.
+Also measured (``per_kernel``): C2 (one fused elementwise kernel), C3
+softmax (4 kernels), the 4096^3 matmul, C4 literal and the fused diamond
+variant, C5 attention (32 heads; each of the 5 per-head kernels launched
+once for all heads, ``api.run_batch``), each kernel against its roofline.
 
-``cpu_baseline``: the CPU oracle (NumPy, single-threaded ufuncs) evaluating
-the same C2 expression on the same full-size inputs for ~10 s on the host;
-``per_config`` the other configurations in float32 NumPy.  ``end_to_end``:
-``api.run`` wall times for C2 and C3 (host transfers included).
+``cpu_baseline``: the same C4 expression on the host's cores in float32 --
+the CPU oracle's op table (``oracle/ir_eval.py``; elementwise ops split over
+row blocks on a thread pool) with NumPy/OpenBLAS sgemm, and beside it
+torch on the CPU -- both pinned to the same thread count; ``per_config``
+does the same for every other configuration.  ``end_to_end``: ``api.run``
+wall times for C2 and C3 (host transfers included).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|fragments|ceilings]
        [--no-extra] [--no-cpu] [--no-flush] [--calibrate-copy]
@@ -334,116 +342,174 @@ def check_c2(prep: Prepared) -> float:
     return float(err.max())
 
 
-def cpu_baseline_c2(ops, budget_s: float = 10.0) -> dict:
-    """Time the CPU oracle on the full C2 inputs for about ``budget_s``."""
-    from oracle.ir_eval import apply_elementwise
-
-    a, b, c, d = (ops.uploads[k] for k in "abcd")
-
-    def once():
-        t = apply_elementwise("mul", a, b)
-        t = apply_elementwise("add", t, c)
-        t = apply_elementwise("negate", t)
-        t = apply_elementwise("exp", t)
-        t = apply_elementwise("add", t, np.float32(1.0))
-        t = apply_elementwise("recip", t)
-        return apply_elementwise("mul", t, d)
-
-    once()
-    n, t0 = 0, time.perf_counter()
-    times = []
-    while time.perf_counter() - t0 < budget_s or n < 3:
-        s = time.perf_counter()
-        once()
-        times.append(time.perf_counter() - s)
-        n += 1
-    med = float(np.median(times))
-    return {
-        "value": round(335_544_320 / med / 1e9, 3),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"full C2 inputs (4 x 4096x4096 fp32), oracle/ir_eval.py NumPy ufuncs, {n} evaluations, median {med*1e3:.1f} ms",
-    }
+def cpu_cores() -> int:
+    """Host threads the CPU baselines use: the process's CPU affinity,
+    capped by ``OMP_NUM_THREADS`` when set (the GPU boxes set it to the
+    one-GPU share of the host)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
 
 
-def _blas_threads() -> int:
-    try:
-        import threadpoolctl
-
-        info = [p for p in threadpoolctl.threadpool_info() if p.get("user_api") == "blas"]
-        if info:
-            return int(info[0]["num_threads"])
-    except ImportError:
-        pass
-    return len(os.sched_getaffinity(0))
+def _split_rows(fn, pool, cores, *arrays):
+    """``fn`` over row blocks of equally shaped arrays on ``pool`` (NumPy
+    ufuncs release the GIL), results stacked in row order."""
+    rows = arrays[0].shape[0]
+    step = -(-rows // cores)
+    parts = [pool.submit(fn, *(a[r : r + step] for a in arrays)) for r in range(0, rows, step)]
+    return np.concatenate([p.result() for p in parts], axis=0)
 
 
-def cpu_baseline_config(label: str, made, per_kernel: list[dict], budget_s: float = 3.0) -> dict | None:
-    """Time one whole configuration on the host CPU in float32: the
-    oracle's elementwise ops (NumPy ufuncs, one thread), NumPy's float32 row
-    reductions, and NumPy float32 matmuls (OpenBLAS sgemm on its thread
-    pool).  At least two evaluations after one warm-up, about ``budget_s``.
-    Throughput uses the configuration's algorithmic work: the matmul flops
-    when it has matmuls, else the kernels' algorithmic bytes."""
-    from oracle.ir_eval import apply_elementwise
+def _numpy_program(label: str, made, pool, cores):
+    """The configuration as one float32 expression over the oracle's op
+    table (``oracle/ir_eval.apply_elementwise``), elementwise work split over
+    row blocks on the thread pool, matmuls on NumPy's OpenBLAS sgemm."""
+    from oracle.ir_eval import apply_elementwise as ew
 
     f32 = np.float32
-    sig = lambda t: apply_elementwise("recip", apply_elementwise("add", apply_elementwise("exp", apply_elementwise("negate", t)), f32(1.0)))
+    sig = lambda t: ew("recip", ew("add", ew("exp", ew("negate", t)), f32(1.0)))
 
-    def softmax_rows(x):
+    def softmax_block(x):
         m = np.max(x, axis=-1, keepdims=True)
-        e = apply_elementwise("exp", apply_elementwise("subtract", x, m))
-        return apply_elementwise("div", e, np.sum(e, axis=-1, keepdims=True, dtype=f32))
+        e = ew("exp", ew("subtract", x, m))
+        return ew("div", e, np.sum(e, axis=-1, keepdims=True, dtype=f32))
 
+    par = lambda fn, *a: _split_rows(fn, pool, cores, *a)
+    if label.startswith("C2"):
+        a, b, c, d = (made.uploads[k] for k in "abcd")
+        return lambda: par(lambda a, b, c, d: ew("mul", sig(ew("add", ew("mul", a, b), c)), d), a, b, c, d)
     if label.startswith("C3"):
         x = made.uploads["x"]
-        once = lambda: softmax_rows(x)
-    elif label.startswith("matmul"):
+        return lambda: par(softmax_block, x)
+    if label.startswith("matmul"):
         a, b = made.uploads["A"], made.uploads["B"]
-        once = lambda: a @ b
-    elif label.startswith("C4"):
+        return lambda: a @ b
+    if label.startswith("C4"):
         u = made.uploads
 
         def once():
             h1, h2 = u["X"] @ u["W1"], u["X"] @ u["W2"]
             if "W3" not in u:  # the diamond variant stops at the product
-                return apply_elementwise("mul", h1, h2)
-            z = apply_elementwise("mul", apply_elementwise("mul", h1, sig(h1)), h2)
+                return par(lambda p, q: ew("mul", p, q), h1, h2)
+            z = par(lambda p, q: ew("mul", ew("mul", p, sig(p)), q), h1, h2)
             return z @ u["W3"]
 
-    elif label.startswith("C5"):
+        return once
+    if label.startswith("C5"):
         q, k, v = (np.stack([p.uploads[n] for p in made]) for n in "QKV")
         kt = k.transpose(0, 2, 1)
         scale = f32(1.0 / np.sqrt(q.shape[-1]))
-        once = lambda: softmax_rows(apply_elementwise("mul", q @ kt, scale)) @ v
-    else:
-        return None
+        return lambda: par(lambda s: softmax_block(ew("mul", s, scale)), q @ kt) @ v
+    return None
+
+
+def _torch_program(label: str, made):
+    """The same expression in torch on the CPU (float32, intra-op threads)."""
+    import torch
+
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    if label.startswith("C2"):
+        a, b, c, d = (t(made.uploads[k]) for k in "abcd")
+        return lambda: torch.reciprocal(torch.exp(-(a * b + c)) + 1.0) * d
+    if label.startswith("C3"):
+        x = t(made.uploads["x"])
+
+        def once():
+            e = torch.exp(x - x.amax(dim=-1, keepdim=True))
+            return e / e.sum(dim=-1, keepdim=True)
+
+        return once
+    if label.startswith("matmul"):
+        a, b = t(made.uploads["A"]), t(made.uploads["B"])
+        return lambda: a @ b
+    if label.startswith("C4"):
+        u = {k: t(v) for k, v in made.uploads.items()}
+
+        def once():
+            h1, h2 = u["X"] @ u["W1"], u["X"] @ u["W2"]
+            if "W3" not in u:
+                return h1 * h2
+            return (h1 * torch.reciprocal(torch.exp(-h1) + 1.0) * h2) @ u["W3"]
+
+        return once
+    if label.startswith("C5"):
+        q, k, v = (t(np.stack([p.uploads[n] for p in made])) for n in "QKV")
+        kt = k.transpose(1, 2)
+        scale = float(np.float32(1.0 / np.sqrt(q.shape[-1])))
+
+        def once():
+            s = (q @ kt) * scale
+            e = torch.exp(s - s.amax(dim=-1, keepdim=True))
+            return (e / e.sum(dim=-1, keepdim=True)) @ v
+
+        return once
+    return None
+
+
+def _time_cpu(once, budget_s: float) -> tuple[float, int]:
+    """Median seconds of ``once()`` over at least 3 runs after one warm-up,
+    running for about ``budget_s``."""
+    once()
+    times, t0 = [], time.perf_counter()
+    while len(times) < 3 or time.perf_counter() - t0 < budget_s:
+        s = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - s)
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline_config(label: str, made, per_kernel: list[dict], budget_s: float = 3.0) -> dict | None:
+    """Time one whole configuration on the host CPU in float32, on
+    ``cpu_cores()`` threads: the oracle-op-table NumPy expression (OpenBLAS
+    and the elementwise thread pool both pinned to that count) and, beside
+    it, torch on the CPU (``torch.set_num_threads`` to the same count).
+    Throughput uses the configuration's algorithmic work: the matmul flops
+    when it has matmuls, else the kernels' algorithmic bytes."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import threadpoolctl
+    import torch
+
+    cores = cpu_cores()
     mine = [k for k in per_kernel if k["config"] == label]
+    if not mine:
+        return None
     if any(k["bound"] == "mfma" for k in mine):
         work, unit, div = sum(k["work"] for k in mine if k["bound"] == "mfma"), "TFLOP/s", 1e12
     else:
         work, unit, div = sum(k["work"] for k in mine), "GB/s", 1e9
-    once()
-    times, t0 = [], time.perf_counter()
-    while len(times) < 2 or time.perf_counter() - t0 < budget_s:
-        s = time.perf_counter()
-        once()
-        times.append(time.perf_counter() - s)
-    med = float(np.median(times))
+    with ThreadPoolExecutor(cores) as pool, threadpoolctl.threadpool_limits(cores):
+        once = _numpy_program(label, made, pool, cores)
+        if once is None:
+            return None
+        med, n = _time_cpu(once, budget_s)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        tmed, tn = _time_cpu(_torch_program(label, made), budget_s)
+    finally:
+        torch.set_num_threads(prev)
     gpu_ms = sum(k["ms_mean"] for k in mine)
-    has_mm = unit == "TFLOP/s"
     return {
         "config": label,
         "value": round(work / med / div, 4),
         "unit": unit,
-        "cores": _blas_threads() if has_mm else 1,
+        "cores": cores,
         "kind": "port",
-        "sample": f"whole configuration, full inputs, NumPy float32 ({'OpenBLAS sgemm + ' if has_mm else ''}"
-        f"single-thread ufuncs), {len(times)} evaluations, median {med*1e3:.1f} ms",
+        "sample": f"whole configuration on the full inputs, float32: oracle op table over NumPy "
+        f"(OpenBLAS sgemm and a {cores}-thread elementwise pool), {n} evaluations, median {med * 1e3:.1f} ms",
         "ms": round(med * 1e3, 3),
+        "torch_cpu": {
+            "value": round(work / tmed / div, 4),
+            "unit": unit,
+            "cores": cores,
+            "ms": round(tmed * 1e3, 3),
+            "sample": f"torch {torch.__version__} CPU float32, {cores} intra-op threads, {tn} evaluations",
+        },
         "gpu_kernels_ms": round(gpu_ms, 4),
-        "gpu_over_cpu": round(med * 1e3 / gpu_ms, 1) if gpu_ms > 0 else None,
+        "gpu_over_cpu": round(min(med, tmed) * 1e3 / gpu_ms, 1) if gpu_ms > 0 else None,
     }
 
 
@@ -599,20 +665,134 @@ def fragment_benches(steps: int, flusher) -> list[dict]:
     return out
 
 
-def read_profile_traffic(name: str) -> float | None:
-    """HBM bytes per launch of the C2 kernel from the committed rocprofv3
-    PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated)."""
+def read_profile_traffic(config: str, kernel: str, name: str = "bench_kernels_pmc.txt") -> float | None:
+    """HBM bytes per launch of ``kernel`` in ``config`` from the committed
+    rocprofv3 PMC summary: its table row ``config  kernel  algorithmic
+    read written ...`` (FETCH_SIZE and WRITE_SIZE, copy-kernel calibrated),
+    read + written.  None when the summary has no such row."""
+    import re
+
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
+    pat = re.compile(r"^(.+?)\s{2,}(\S+)\s+(\(mfma\)|\d+)\s+(\d+)\s+(\d+)")
     with open(path, encoding="utf-8") as f:
         for line in f:
-            if line.startswith("traffic_bytes_per_launch:"):
-                try:
-                    return float(line.split(":", 1)[1].strip())
-                except ValueError:
-                    return None
+            m = pat.match(line)
+            if m and m.group(1).strip() == config and m.group(2) == kernel:
+                return float(int(m.group(4)) + int(m.group(5)))
     return None
+
+
+C4_LABEL = "C4 MLP literal"
+C4_FLOPS = 3 * 2 * 4096 * 4096 * 11008  # 1.108 TFLOP of matmul work per step
+
+
+def check_c4(prep: Prepared, rows: int = 64) -> float:
+    """Sampled rows of the C4 output against float64 from the GPU's own
+    ``z = h1 * s * h2`` (the W3 kernel's A operand): the whole-output checks
+    are GPU tests; this guards the timed run.  Returns the max abs error."""
+    from tests.matmul_check import check_matmul
+
+    pick = np.sort(np.random.default_rng(0).choice(4096, rows, replace=False))
+    h1, s, h2, out = (prep.download(k, (4096, 11008) if k != "out" else (4096, 4096)) for k in ("h1", "s", "h2", "out"))
+    z = (h1[pick] * s[pick]) * h2[pick]
+    w3 = prep.ops.uploads["W3"]
+    check_matmul(out[pick], z, w3, "C4 out (sampled rows)")
+    return float(np.abs(out[pick].astype(np.float64) - z.astype(np.float64) @ w3.astype(np.float64)).max())
+
+
+def headline_c4(args, flush, info) -> tuple[dict, dict]:
+    """Time ``args.steps`` C4 steps (flush, then the 4 kernels back to back
+    between stream markers).  Returns the JSON line and the per-kernel
+    records of the in-step kernel times."""
+    from metellus_amd.runtime import hip_backend
+
+    prep = Prepared(_c4(False))
+    n = len(prep.groups)
+    assert n == 4 and n + 1 <= 16, [g.kernel.function_name for g in prep.groups]
+    for i in range(n):
+        warm_up(lambda timed, i=i: prep.launch(i, timed=timed), flush, args.warmup)
+    hip_backend.synchronize()
+    step_ms, kern_ms = [], [[] for _ in range(n)]
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        if flush is not None:
+            flush.flush()
+        hip_backend.mark(0)
+        for i in range(n):
+            prep.launch(i)
+            hip_backend.mark(i + 1)
+        step_ms.append(hip_backend.mark_elapsed(0, n))
+        for i in range(n):
+            kern_ms[i].append(hip_backend.mark_elapsed(i, i + 1))
+    hip_backend.synchronize()
+    wall = time.perf_counter() - t0
+    hip_backend.check_workspace()
+    err = check_c4(prep)
+    ms = float(np.mean(step_ms))
+    tflops = C4_FLOPS / (ms * 1e-3) / 1e12
+    records = []
+    for i, g in enumerate(prep.groups):
+        bound, work = kernel_work(g, prep.owner)
+        mean = float(np.mean(kern_ms[i]))
+        if bound == "hbm":
+            achieved, peak, unit = work / (mean * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        else:
+            achieved, peak, unit = work / (mean * 1e-3) / 1e12, FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
+        records.append({
+            "kernel": g.kernel.function_name, "config": C4_LABEL + " (in-step)", "strategy": g.strategy.value,
+            "grid": list(g.grid), "threads": list(g.threads), "ms_mean": round(mean, 5),
+            "ms_min": round(float(np.min(kern_ms[i])), 5), "ms_median": round(float(np.median(kern_ms[i])), 5),
+            "bound": bound, "work": work, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4),
+        })
+    dom = max(records, key=lambda r: r["ms_mean"])
+    traffic = read_profile_traffic(C4_LABEL, dom["kernel"])
+    line = {
+        "metric": "fused-kernel fp32 TFLOP/s & HBM GB/s (% of roofline), 1×MI355X",
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (N(0, 1/sqrt(fan_in)), numpy seed 3)",
+        "config": {
+            "workload": "C4: out = (silu(X@W1) * (X@W2)) @ W3, X 4096x4096, W1/W2 4096x11008, W3 11008x4096 fp32 "
+            "(BASELINE.json configs[3], the largest configuration); 4 fused kernels per step",
+            "kernels": [g.kernel.function_name for g in prep.groups],
+            "flops_per_step": C4_FLOPS,
+            "step_ms_min": round(float(np.min(step_ms)), 5),
+            "step_ms_median": round(float(np.median(step_ms)), 5),
+            "fraction_of_fp32_mfma_peak": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            "cache_flush_between_steps": flush is not None,
+            "wall_ms_per_step_incl_flush": round(wall * 1e3 / args.steps, 4),
+            "max_abs_err_vs_float64_sampled_rows": err,
+            "device": info["arch"],
+            "parallelism": "1 GPU",
+        },
+        "roofline": {
+            "kernel": dom["kernel"],
+            "bound": dom["bound"],
+            "achieved": dom["achieved"],
+            "peak": dom["peak"],
+            "unit": dom["unit"],
+            "frac": dom["frac"],
+            "traffic": traffic,
+        },
+    }
+    log(f"[bench] C4: {ms:.4f} ms/step, {tflops:.2f} TFLOP/s ({100 * tflops / FP32_MFMA_PEAK_TFLOPS:.1f}% of "
+        f"fp32 MFMA peak); dominant {dom['kernel']} {dom['ms_mean']:.4f} ms ({100 * dom['frac']:.1f}%)")
+    for r in records:
+        log(f"[bench]   {r['kernel']}: {r['ms_mean']:.4f} ms  {r['achieved']:.1f} {r['unit']} ({100 * r['frac']:.1f}%)")
+    made = prep.ops
+    prep.release()
+    return line, {"records": records, "made": made}
 
 
 def main() -> int:
@@ -646,72 +826,23 @@ def main() -> int:
     log(f"[bench] device {info}")
     flush = None if args.no_flush else Flusher()
 
-    # ---- headline: C2 ------------------------------------------------------
+    # ---- headline: C4 literal ----------------------------------------------
     only = args.only
     line = None
     per_config: list[dict] = []
     cpu_configs: list[dict] = []
-    if only in (None, "c2"):
-        log("[bench] C2 sigmoid chain 4096x4096: preparing")
-        prep = time_prep = Prepared(_c2())
-        assert len(prep.groups) == 1
-        warm_up(lambda timed: prep.launch(0, timed=timed), flush, args.warmup)
-        hip_backend.synchronize()
-        kernel_ms = []
-        t0 = time.perf_counter()
-        for s in range(args.steps):
-            if flush is not None:
-                flush.flush()
-            kernel_ms.append(prep.launch(0, timed=True))
-        hip_backend.synchronize()
-        wall = time.perf_counter() - t0
-        err = check_c2(prep)
-        ms = float(np.mean(kernel_ms))
-        bytes_per_step = 335_544_320
-        gbs = bytes_per_step / (ms * 1e-3) / 1e9
-        traffic = read_profile_traffic("elementwise_out_fused_c2_pmc.txt")
-        g = prep.groups[0]
-        line = {
-            "metric": "fused-kernel fp32 TFLOP/s & HBM GB/s (% of roofline), 1×MI355X",
-            "value": round(gbs, 2),
-            "unit": "GB/s",
-            "n_gpus": 1,
-            "steps": args.steps,
-            "warmup": args.warmup,
-            "ms_per_step": round(ms, 5),
-            "higher_is_better": True,
-            "scaling": "weak",
-            "vs_baseline": None,
-            "dtype": "f32",
-            "data": "synthetic (N(0,1), numpy seed 1)",
-            "config": {
-                "workload": "C2: out = sigmoid(a*b + c) * d, 4 fp32 inputs 4096x4096, one fused kernel",
-                "kernel": g.kernel.function_name,
-                "strategy": g.strategy.value,
-                "grid": list(g.grid),
-                "threads": list(g.threads),
-                "bytes_per_step": bytes_per_step,
-                "cache_flush_between_steps": flush is not None,
-                "wall_ms_per_step_incl_flush": round(wall * 1e3 / args.steps, 4),
-                "max_abs_err_vs_oracle_sampled_rows": err,
-                "device": info["arch"],
-                "parallelism": "1 GPU",
-            },
-            "roofline": {
-                "bound": "hbm",
-                "achieved": round(gbs, 2),
-                "peak": HBM_PEAK_GBS,
-                "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "traffic": traffic,
-            },
-        }
-        log(f"[bench] C2: {ms:.4f} ms/step, {gbs:.1f} GB/s ({100*gbs/HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+    if only in (None, "c4"):
+        log("[bench] C4 MLP block (headline): preparing")
+        line, head = headline_c4(args, flush, info)
+        per_config += head["records"]
         if not args.no_cpu:
-            log("[bench] CPU baseline (oracle, ~10 s)")
-            line["cpu_baseline"] = cpu_baseline_c2(prep.ops)
-        prep.release()
-        del time_prep
+            log(f"[bench] C4 CPU baseline on {cpu_cores()} threads (~20 s)")
+            cpu = cpu_baseline_config(C4_LABEL + " (in-step)", head["made"], per_config, budget_s=10.0)
+            cpu["config"] = C4_LABEL
+            line["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "ms", "torch_cpu")}
+            log(f"[bench] C4 CPU: {cpu['value']} TFLOP/s oracle/NumPy, {cpu['torch_cpu']['value']} TFLOP/s torch "
+                f"on {cpu['cores']} threads")
+        del head
 
     if args.calibrate_copy:
         log("[bench] copy calibration: 64 MiB in, 64 MiB out")
@@ -730,9 +861,11 @@ def main() -> int:
         per_config += ceiling_benches(max(3, args.steps), flush)
 
     # ---- other configs -----------------------------------------------------
-    if (not args.no_extra and only is None) or only not in (None, "c2", "fragments"):
+    if (not args.no_extra and only is None) or only not in (None, "fragments"):
         extra_steps = max(3, args.steps)
         todo = []
+        if only in (None, "c2"):
+            todo.append(("C2 sigmoid chain 4096x4096", _c2))
         if only in (None, "c3"):
             todo.append(("C3 softmax 8192x8192", _c3))
         if only in (None, "gemm"):
@@ -747,8 +880,10 @@ def main() -> int:
             made = make()
             prep = PreparedBatch(made) if isinstance(made, list) else Prepared(made)
             per_config += time_kernels(prep, extra_steps, 2, flush, label)
+            if label.startswith("C2"):
+                check_c2(prep)
             prep.release()
-            if not args.no_cpu:
+            if not args.no_cpu and not (label == C4_LABEL and line is not None):  # the headline timed C4 already
                 cpu = cpu_baseline_config(label, made, per_config)
                 if cpu is not None:
                     cpu_configs.append(cpu)

@@ -103,6 +103,16 @@ int mt_compile_only(const char* source, const char* options, const char* target,
 int mt_launch(uint64_t kernel, const uint64_t* buffers, int nbuf, const uint32_t* dims, int ndims,
               int dims_slot, const uint32_t* grid, const uint32_t* block, int timed, float* ms);
 
+/* Timing markers (no counterpart in the reference, whose run_kernel times
+ * one dispatch at a time): record marker `slot` (0..15) on the shim's
+ * stream, after everything queued so far.  The events skip the system-scope
+ * release fence, like timed launches. */
+int mt_mark(int slot);
+
+/* Wait for marker `to`, then *ms = GPU time from marker `from` to `to`:
+ * several launches queued back to back are timed as one sequence. */
+int mt_mark_elapsed(int from, int to, float* ms);
+
 /* Wait for all queued work on the shim's stream. */
 int mt_sync(void);
 

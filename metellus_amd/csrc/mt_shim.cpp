@@ -74,6 +74,7 @@ struct State {
     hipStream_t stream = nullptr;
     hipEvent_t ev_start = nullptr;
     hipEvent_t ev_stop = nullptr;
+    hipEvent_t marks[16] = {};  // mt_mark / mt_mark_elapsed
     std::string arch;  // full target id of device 0
     int cu_count = 0;
     int clock_khz = 0;
@@ -285,6 +286,7 @@ int init_locked(State& s) {
     // synchronises it.
     MT_HIP(hipEventCreateWithFlags(&s.ev_start, hipEventDisableSystemFence));
     MT_HIP(hipEventCreateWithFlags(&s.ev_stop, hipEventDisableSystemFence));
+    for (auto& m : s.marks) MT_HIP(hipEventCreateWithFlags(&m, hipEventDisableSystemFence));
     // Keep memory released by hipFreeAsync in the device's pool instead of
     // returning it at each synchronisation, so buffers of repeated runs are
     // served from the pool.
@@ -731,6 +733,26 @@ int mt_workspace_check(uint32_t* error) {
         MT_HIP(hipStreamSynchronize(s.stream));
     }
     *error = word;
+    return 0;
+}
+
+int mt_mark(int slot) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    if (slot < 0 || slot >= 16) return fail("mt_mark: slot must be in [0, 16)");
+    MT_HIP(hipEventRecord(s.marks[slot], s.stream));
+    return 0;
+}
+
+int mt_mark_elapsed(int from, int to, float* ms) {
+    if (!ms) return fail("mt_mark_elapsed: null output");
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    if (from < 0 || from >= 16 || to < 0 || to >= 16) return fail("mt_mark_elapsed: slots must be in [0, 16)");
+    MT_HIP(hipEventSynchronize(s.marks[to]));
+    MT_HIP(hipEventElapsedTime(ms, s.marks[from], s.marks[to]));
     return 0;
 }
 

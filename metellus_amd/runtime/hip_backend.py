@@ -44,6 +44,8 @@ EXPORTED_SYMBOLS = (
     "mt_compile",
     "mt_compile_only",
     "mt_launch",
+    "mt_mark",
+    "mt_mark_elapsed",
     "mt_sync",
     "mt_cache_stats",
     "mt_workspace",
@@ -101,6 +103,8 @@ def _load():
                  ctypes.c_int, ctypes.POINTER(ctypes.c_float)],
                 ctypes.c_int,
             ),
+            "mt_mark": ([ctypes.c_int], ctypes.c_int),
+            "mt_mark_elapsed": ([ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_float)], ctypes.c_int),
             "mt_sync": ([], ctypes.c_int),
             "mt_cache_stats": ([ctypes.POINTER(_u64), ctypes.POINTER(_u64)], ctypes.c_int),
             "mt_workspace": ([ctypes.c_size_t, ctypes.POINTER(_u64)], ctypes.c_int),
@@ -146,6 +150,18 @@ def device_info() -> dict:
 
 def synchronize() -> None:
     _check(_load().mt_sync())
+
+
+def mark(slot: int) -> None:
+    """Record timing marker ``slot`` (0..15) on the shim's stream."""
+    _check(_load().mt_mark(int(slot)))
+
+
+def mark_elapsed(first: int, last: int) -> float:
+    """Wait for marker ``last``; GPU milliseconds from ``first`` to ``last``."""
+    ms = ctypes.c_float(0.0)
+    _check(_load().mt_mark_elapsed(int(first), int(last), ctypes.byref(ms)))
+    return float(ms.value)
 
 
 def cache_stats() -> tuple[int, int]:
@@ -291,6 +307,11 @@ def launch(
         )
     )
     return float(ms.value) if timed else None
+
+
+def init() -> None:
+    """Select the device and create the shim's stream (``mt_init``)."""
+    _check(_load().mt_init())
 
 
 def run_kernel(source: str, function_name: str, buffers, grid, threads, *, dims=(), dims_slot=None) -> dict:
