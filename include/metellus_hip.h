@@ -103,6 +103,26 @@ int mt_compile_only(const char* source, const char* options, const char* target,
 int mt_launch(uint64_t kernel, const uint64_t* buffers, int nbuf, const uint32_t* dims, int ndims,
               int dims_slot, const uint32_t* grid, const uint32_t* block, int timed, float* ms);
 
+/* Allocation-free variant of mt_launch.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * Same parameters and kernel-parameter order as mt_launch, without timing;
+ * when scratch_bytes > 0 (a stream-K kernel's workspace_bytes) the kernel's
+ * last parameter is the library's static device scratch instead of the
+ * mt_workspace buffer.  The scratch holds at most 64 MiB + 4096 bytes
+ * (larger requests fail with an error and launch nothing); its 4096-byte
+ * flag head is cleared by a small kernel before each such launch.  The call
+ * performs no device or host allocation and requires a prior mt_init (it
+ * fails otherwise).  All calls on one device share its scratch, which keeps
+ * the last launch's contents: they are ordered by the shim's single stream,
+ * but launches that overlap on one GPU by other means (a captured graph
+ * replayed on another stream) race.  error == NULL: asynchronous.
+ * Otherwise the call waits for the launch and stores the scratch's error
+ * word (nonzero: a stream-K wait gave up and the results are invalid). */
+int mt_launch_noalloc(uint64_t kernel, const uint64_t* buffers, int nbuf, const uint32_t* dims, int ndims,
+                      int dims_slot, const uint32_t* grid, const uint32_t* block, size_t scratch_bytes,
+                      uint32_t* error);
+
 /* Timing markers (no counterpart in the reference, whose run_kernel times
  * one dispatch at a time): record marker `slot` (0..15) on the shim's
  * stream, after everything queued so far.  The events skip the system-scope

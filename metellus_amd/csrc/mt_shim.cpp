@@ -9,9 +9,12 @@
 //     text -- the reference recompiled MSL on every dispatch
 //     (metal_backend.mm:188-207);
 //   * hipModuleLaunchKernel on a single stream, asynchronous unless timed --
-//     the reference waited after every dispatch (metal_backend.mm:226-227).
+//     the reference waited after every dispatch (metal_backend.mm:226-227);
+//   * mt_launch_noalloc: the same launch for callers that cannot allocate,
+//     with stream-K kernels' workspace in a static device array (`scratch`).
 //
-// Pure host code: it contains no device kernels of its own.
+// Its only device code is that array and a word-clearing kernel; every
+// compute kernel is generated and compiled at run time.
 
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
@@ -95,12 +98,37 @@ struct State {
     // Staging ring for transfers between pageable host memory and the device.
     void* stage[kStages] = {};
     hipEvent_t stage_ev[kStages] = {};
+    // Device address of `scratch` per device id, from hipGetSymbolAddress
+    // with that device current (the shim runs on device 0: entry 0).
+    void* scratch_ptr[16] = {};
 };
 
 // Workspace layout shared with the device library (MT_WS_HEAD): flag words,
 // the last of them the error word, then the partial tiles.
 constexpr size_t kWsHeadBytes = 1024 * sizeof(uint32_t);
 constexpr size_t kWsErrorOffset = 1023 * sizeof(uint32_t);
+
+// ---- static scratch of the allocation-free launch ---------------------------
+//
+// The workspace of stream-K kernels launched by mt_launch_noalloc: the
+// 4 KiB flag head, then partial tiles -- 64 MiB holds one 256x256 fp32 tile
+// (or two 256x128 accumulator sets) for each of 256 persistent workgroups,
+// what the C4 matmuls use.  Each device the library runs on holds its own
+// copy from module load until the process ends.  In host code `scratch` is
+// only a symbol: its device address comes from hipGetSymbolAddress (at
+// init) and is the only form passed to kernels.
+constexpr size_t kScratchBytes = kWsHeadBytes + (size_t(64) << 20);
+static __device__ __align__(256) uint32_t scratch[kScratchBytes / sizeof(uint32_t)];
+
+// Zero n words (vector stores, one per lane): the scratch head before each
+// allocation-free stream-K launch.  A kernel instead of hipMemsetAsync, so
+// the launch stays correct when a caller captures it in a graph.
+__global__ void mt_clear_words(uint32_t* p, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+constexpr int kMaxLaunchBuffers = 64;
 
 constexpr size_t kHostGranule = size_t(64) << 10;     // pinned blocks are multiples of 64 KiB
 constexpr size_t kHostCacheLimit = size_t(1) << 30;   // at most 1 GiB of returned blocks kept
@@ -272,6 +300,7 @@ int init_locked(State& s) {
                     (e != hipSuccess ? hipGetErrorString(e) : "device count is 0"));
     }
     MT_HIP(hipSetDevice(0));
+    MT_HIP(hipGetSymbolAddress(&s.scratch_ptr[0], HIP_SYMBOL(scratch)));
     hipDeviceProp_t prop;
     MT_HIP(hipGetDeviceProperties(&prop, 0));
     s.arch = prop.gcnArchName;
@@ -688,6 +717,66 @@ int mt_launch(uint64_t kernel, const uint64_t* buffers, int nbuf, const uint32_t
         float t = 0.f;
         MT_HIP(hipEventElapsedTime(&t, s.ev_start, s.ev_stop));
         if (ms) *ms = t;
+    }
+    return 0;
+}
+
+int mt_launch_noalloc(uint64_t kernel, const uint64_t* buffers, int nbuf, const uint32_t* dims, int ndims,
+                      int dims_slot, const uint32_t* grid, const uint32_t* block, size_t scratch_bytes,
+                      uint32_t* error) {
+    if (!grid || !block) return fail("mt_launch_noalloc: grid and block are required");
+    if (ndims < 0 || ndims > kMaxDims) return fail("mt_launch_noalloc: at most 16 dims");
+    if (nbuf < 0 || nbuf > kMaxLaunchBuffers) return fail("mt_launch_noalloc: at most 64 buffers");
+    if (dims_slot < 0 || dims_slot > nbuf) return fail("mt_launch_noalloc: bad dims slot");
+    if (scratch_bytes > kScratchBytes)
+        return fail("mt_launch_noalloc: the kernel needs " + std::to_string(scratch_bytes) +
+                    " bytes of scratch; the static scratch holds " + std::to_string(kScratchBytes));
+    if (scratch_bytes != 0 && scratch_bytes < kWsHeadBytes)
+        return fail("mt_launch_noalloc: a scratch request covers at least the 4096-byte flag head");
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    // Initialisation creates the stream and events; this entry point does
+    // not do it on a caller's behalf.
+    if (!s.ready) return fail("mt_launch_noalloc: call mt_init first");
+    if (kernel == 0 || kernel > s.kernels.size()) return fail("mt_launch_noalloc: unknown kernel handle");
+    for (int i = 0; i < 3; ++i) {
+        if (grid[i] == 0 || block[i] == 0) return fail("mt_launch_noalloc: zero grid or block extent");
+    }
+    if (static_cast<uint64_t>(block[0]) * block[1] * block[2] > 1024)
+        return fail("mt_launch_noalloc: more than 1024 lanes per workgroup");
+    void* ptrs[kMaxLaunchBuffers];
+    for (int i = 0; i < nbuf; ++i) {
+        Buffer b;
+        if (lookup(s, buffers[i], &b)) return 1;
+        ptrs[i] = b.ptr;
+    }
+    DimsArg d{};
+    for (int i = 0; i < ndims; ++i) d.v[i] = dims[i];
+    void* params[kMaxLaunchBuffers + 2];
+    int np = 0;
+    for (int i = 0; i <= nbuf; ++i) {
+        if (i == dims_slot) params[np++] = &d;
+        if (i < nbuf) params[np++] = &ptrs[i];
+    }
+    void* ws = s.scratch_ptr[0];
+    if (scratch_bytes != 0) {
+        // Flags and the error word start at 0 on every call: a previous
+        // launch that gave up waiting may have left flags raised.
+        constexpr uint32_t words = kWsHeadBytes / sizeof(uint32_t);
+        hipLaunchKernelGGL(mt_clear_words, dim3(words / 256), dim3(256), 0, s.stream, static_cast<uint32_t*>(ws),
+                           words);
+        MT_HIP(hipGetLastError());
+        params[np++] = &ws;
+    }
+    const Kernel& k = s.kernels[kernel - 1];
+    MT_HIP(hipModuleLaunchKernel(k.function, grid[0], grid[1], grid[2], block[0], block[1], block[2], 0,
+                                 s.stream, params, nullptr));
+    if (error) {
+        *error = 0;
+        if (scratch_bytes != 0)
+            MT_HIP(hipMemcpyAsync(error, static_cast<char*>(ws) + kWsErrorOffset, sizeof(uint32_t),
+                                  hipMemcpyDeviceToHost, s.stream));
+        MT_HIP(hipStreamSynchronize(s.stream));
     }
     return 0;
 }

@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "mt_compile",
     "mt_compile_only",
     "mt_launch",
+    "mt_launch_noalloc",
     "mt_mark",
     "mt_mark_elapsed",
     "mt_sync",
@@ -101,6 +102,11 @@ def _load():
             "mt_launch": (
                 [_u64, ctypes.POINTER(_u64), ctypes.c_int, _u32p, ctypes.c_int, ctypes.c_int, _u32p, _u32p,
                  ctypes.c_int, ctypes.POINTER(ctypes.c_float)],
+                ctypes.c_int,
+            ),
+            "mt_launch_noalloc": (
+                [_u64, ctypes.POINTER(_u64), ctypes.c_int, _u32p, ctypes.c_int, ctypes.c_int, _u32p, _u32p,
+                 ctypes.c_size_t, _u32p],
                 ctypes.c_int,
             ),
             "mt_mark": ([ctypes.c_int], ctypes.c_int),
@@ -307,6 +313,32 @@ def launch(
         )
     )
     return float(ms.value) if timed else None
+
+
+def launch_noalloc(kernel: int, buffers, dims, dims_slot: int, grid, threads, scratch: int = 0,
+                   wait: bool = True) -> int | None:
+    """``mt_launch_noalloc``: launch without allocating; a stream-K kernel
+    (``scratch`` = its ``workspace_bytes``) gets the library's static scratch
+    as its last parameter.  ``wait``: synchronise and return the scratch's
+    error word (0 unless a stream-K wait gave up); otherwise None."""
+    handles = [_handle_of(b) for b in buffers]
+    nb = len(handles)
+    bufs = (_u64 * max(nb, 1))(*handles)
+    dims_l = [int(d) for d in dims]
+    for d in dims_l:
+        if not 0 <= d < 2**32:
+            raise ValueError(f"dim value {d} does not fit in uint32")
+    dims_a = (ctypes.c_uint32 * max(len(dims_l), 1))(*dims_l)
+    grid_a = (ctypes.c_uint32 * 3)(*[int(g) for g in grid])
+    block_a = (ctypes.c_uint32 * 3)(*[int(t) for t in threads])
+    err = ctypes.c_uint32(0)
+    _check(
+        _load().mt_launch_noalloc(
+            kernel, bufs, nb, dims_a, len(dims_l), int(dims_slot), grid_a, block_a, int(scratch),
+            ctypes.byref(err) if wait else None,
+        )
+    )
+    return int(err.value) if wait else None
 
 
 def init() -> None:
