@@ -300,9 +300,10 @@ class MatmulComputeFragment:
     name: str = "matmul_compute"
     kind: str = "compute"
 
-    def render_stage(self, stage: str | None) -> str:
+    def render_stage(self, stage: str | None, hook: str | None = None) -> str:
         """MFMAs over LDS buffer ``stage`` of double-buffered tiles, or over
-        single-buffered tiles when ``stage`` is None."""
+        single-buffered tiles when ``stage`` is None; ``hook`` names a
+        callable run at each group of 4 k-steps (``mt_mfma_tile``)."""
         t = self.config.tile
         at, bt = self.config.a_tile_name, self.config.b_tile_name
         a_ptr = f"&{at}[{stage}][wave_m0][0]" if stage is not None else f"&{at}[wave_m0][0]"
@@ -315,9 +316,12 @@ class MatmulComputeFragment:
             aswz = "true" if t.a_layout == "swz" else "false"
             bnm = "true" if t.b_layout == "nswz" else "false"
             flags = f", {aswz}, {bnm}"
+        if hook is not None and not flags:
+            flags = ", false, false"
+        hook_arg = f", {hook}" if hook is not None else ""
         return (
             f"mt_mfma_tile<{t.WM}, {t.WN}, {t.tile_K}, {t.lda}, {t.ldb}{flags}>"
-            f"({a_ptr}, {b_ptr}, acc{self.accumulator_suffix}, lane);"
+            f"({a_ptr}, {b_ptr}, acc{self.accumulator_suffix}, lane{hook_arg});"
         )
 
     def render(self, ctx: CodegenContext) -> str:
@@ -367,6 +371,13 @@ class MatmulMainloopFragment:
     fragments: tuple[KernelFragment, ...]
     K_dim_var: str
     persistent: bool = False
+    # > 0: the next chunk's register-path loads are issued in ``spread``
+    # parts at the first ``spread`` groups of 4 k-steps of the current
+    # chunk's MFMAs (a hook of the first compute fragment) instead of all
+    # before them; direct-to-LDS loads stay before the MFMAs unless
+    # ``spread_dma``.
+    spread: int = 0
+    spread_dma: bool = False
     name: str = "matmul_mainloop"
     kind: str = "compute"
 
@@ -407,6 +418,7 @@ class MatmulMainloopFragment:
                 raise ValueError("a persistent tile loop needs double-buffered LDS tiles")
             return self._render_persistent(loads, computes, body)
         sync = self._sync(loads)
+        spread = self._spread(loads)
         body += [
             f"const unsigned n_chunks = ({kvar} + {tk - 1}u) / {tk}u;",
             "{",
@@ -418,20 +430,51 @@ class MatmulMainloopFragment:
             "for (unsigned kt = 0; kt < n_chunks; ++kt) {",
             "    const unsigned cur = kt & 1u;",
             "    const bool more = kt + 1u < n_chunks;",
-            "    if (more) {",
-            f"        const unsigned k_chunk = (kt + 1u) * {tk}u;",
-            *[f"        {ld.render_fetch(stage='cur ^ 1u')}" for ld in loads],
-            "    }",
-            *[f"    {c.render_stage('cur')}" for c in computes],
+            *self._next_loads(loads, spread, persistent=False),
+            *[f"    {c.render_stage('cur', 'mt_hook' if spread and i == 0 else None)}" for i, c in enumerate(computes)],
             *_guarded("    if (more) {", [f"        {c}" for c in _nonempty(ld.render_commit("cur ^ 1u") for ld in loads)]),
             *[f"    {x}" for x in sync],
             "}",
         ]
         return "{\n" + textwrap.indent("\n".join(body), "    ") + "\n}"
 
+    def _spread(self, loads) -> int:
+        """Hook points the next chunk's spread loads are issued at (0: none,
+        also when no loader is spread)."""
+        if not self.spread or not any(self._is_spread(ld) for ld in loads):
+            return 0
+        return max(1, min(self.spread, self.tile_K // 8))
+
+    def _is_spread(self, ld) -> bool:
+        return self.spread_dma or not getattr(ld, "is_dma", False)
+
+    def _next_loads(self, loads, spread: int, persistent: bool) -> list[str]:
+        """Loop-head lines issuing the next chunk's loads (the next item's
+        first chunk at the end of a persistent item): all of them before
+        the MFMAs, or the spread ones in ``mt_hook``'s parts."""
+
+        def guarded(lds, part, pad):
+            fetch = [ld.render_fetch(stage="cur ^ 1u", part=part) for ld in lds]
+            lines = ["if (more) {", f"    const unsigned k_chunk = (kt + 1u) * {self.tile_K}u;",
+                     *[f"    {x}" for x in fetch]]
+            if persistent:
+                lines += ["} else if (mt_has_next) {", "    const unsigned tile_m0 = mt_next_m0;",
+                          "    const unsigned tile_n0 = mt_next_n0;",
+                          f"    const unsigned k_chunk = mt_next_kb * {self.tile_K}u;", *[f"    {x}" for x in fetch]]
+            return [pad + x for x in (*lines, "}")]
+
+        early = [ld for ld in loads if not (spread and self._is_spread(ld))]
+        out = guarded(early, None, "    ") if early else []
+        if spread:
+            late = [ld for ld in loads if self._is_spread(ld)]
+            out += ["    const auto mt_hook = [&](int mt_q) {", f"        if (mt_q >= {spread}) return;",
+                    *guarded(late, f"mt_q, {spread}", "        "), "    };"]
+        return out
+
     def _render_persistent(self, loads, computes, body: list[str]) -> str:
         tk = self.tile_K
         sync = self._sync(loads)
+        spread = self._spread(loads)
         body += [
             "if (mt_first_tile) {",
             f"    const unsigned k_chunk = mt_kb * {tk}u;",
@@ -442,16 +485,8 @@ class MatmulMainloopFragment:
             "for (unsigned kt = mt_kb; kt < mt_ke; ++kt) {",
             "    const unsigned cur = mt_stage;",
             "    const bool more = kt + 1u < mt_ke;",
-            "    if (more) {",
-            f"        const unsigned k_chunk = (kt + 1u) * {tk}u;",
-            *[f"        {ld.render_fetch(stage='cur ^ 1u')}" for ld in loads],
-            "    } else if (mt_has_next) {",
-            "        const unsigned tile_m0 = mt_next_m0;",
-            "        const unsigned tile_n0 = mt_next_n0;",
-            f"        const unsigned k_chunk = mt_next_kb * {tk}u;",
-            *[f"        {ld.render_fetch(stage='cur ^ 1u')}" for ld in loads],
-            "    }",
-            *[f"    {c.render_stage('cur')}" for c in computes],
+            *self._next_loads(loads, spread, persistent=True),
+            *[f"    {c.render_stage('cur', 'mt_hook' if spread and i == 0 else None)}" for i, c in enumerate(computes)],
             *_guarded("    if (more || mt_has_next) {",
                       [f"        {c}" for c in _nonempty(ld.render_commit("cur ^ 1u") for ld in loads)]),
             *[f"    {x}" for x in sync],

@@ -147,6 +147,17 @@ struct mt_identity {
     MT_INLINE float operator()(float v, unsigned, unsigned) const { return v; }
 };
 
+// Partial fetches.  Every fetch takes an optional (q, Q): it then issues only
+// the loads of part q of Q, slot i of n belonging to part (i * Q) / n, so Q
+// calls with q = 0 .. Q-1 issue every load exactly once (the default 0, 1 is
+// the whole tile).  The mainloop spreads a chunk's loads over the MFMA
+// sequence this way instead of issuing them in one burst: a burst of vector
+// memory instructions holds each wave in load issue while the address units
+// work through it, and its MFMAs wait behind them.
+__host__ __device__ __forceinline__ constexpr bool mt_in_part(int i, int n, int q, int Q) {
+    return Q <= 1 || (i * Q) / n == q;
+}
+
 // Vectorised along columns: cs == 1, rs % 4 == 0, COLS % 4 == 0, clim % 4 == 0.
 template <int ROWS, int COLS, int NT>
 struct mt_tile_colvec {
@@ -157,9 +168,10 @@ struct mt_tile_colvec {
 
     template <bool CHECK, typename F>
     MT_INLINE void fetch(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
-                         unsigned rlim, unsigned clim, unsigned tid, F f) {
+                         unsigned rlim, unsigned clim, unsigned tid, F f, int q = 0, int Q = 1) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
+            if (!mt_in_part(i, PER, q, Q)) continue;
             const unsigned idx = tid + i * NT;
             const unsigned r = idx / CV, c = (idx % CV) * 4u;
             const unsigned gr = row0 + r, gc = col0 + c;
@@ -182,11 +194,12 @@ struct mt_tile_colvec {
     // in-bounds elements only).  Same register layout as fetch().
     template <typename F>
     MT_INLINE void fetch_safe(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
-                              unsigned rlim, unsigned clim, unsigned tid, F f) {
+                              unsigned rlim, unsigned clim, unsigned tid, F f, int q = 0, int Q = 1) {
         const bool aligned =
             ((rs & 3u) == 0u) && ((reinterpret_cast<unsigned long long>(src) & 15ull) == 0ull) && ((col0 & 3u) == 0u);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
+            if (!mt_in_part(i, PER, q, Q)) continue;
             const unsigned idx = tid + i * NT;
             const unsigned r = idx / CV, c = (idx % CV) * 4u;
             const unsigned gr = row0 + r, gc = col0 + c;
@@ -235,9 +248,9 @@ struct mt_tile_colvec {
 
     template <bool CHECK>
     MT_INLINE void fetch_raw(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
-                             unsigned rlim, unsigned clim, unsigned tid) {
+                             unsigned rlim, unsigned clim, unsigned tid, int q = 0, int Q = 1) {
         r0 = row0, c0 = col0, rl = rlim, cl = clim;
-        fetch<CHECK>(src, rs, row0, col0, rlim, clim, tid, mt_identity{});
+        fetch<CHECK>(src, rs, row0, col0, rlim, clim, tid, mt_identity{}, q, Q);
     }
 
     template <int LD, bool CHECK, typename F>
@@ -268,9 +281,10 @@ struct mt_tile_rowvec {
 
     template <bool CHECK, typename F>
     MT_INLINE void fetch(const float* __restrict__ src, unsigned cs, unsigned row0, unsigned col0,
-                         unsigned rlim, unsigned clim, unsigned tid, F f) {
+                         unsigned rlim, unsigned clim, unsigned tid, F f, int q = 0, int Q = 1) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
+            if (!mt_in_part(i, PER, q, Q)) continue;
             const unsigned idx = tid + i * NT;
             const unsigned c = idx / RV, r = (idx % RV) * 4u;
             const unsigned gr = row0 + r, gc = col0 + c;
@@ -305,9 +319,9 @@ struct mt_tile_rowvec {
 
     template <bool CHECK>
     MT_INLINE void fetch_raw(const float* __restrict__ src, unsigned cs, unsigned row0, unsigned col0,
-                             unsigned rlim, unsigned clim, unsigned tid) {
+                             unsigned rlim, unsigned clim, unsigned tid, int q = 0, int Q = 1) {
         r0 = row0, c0 = col0, rl = rlim, cl = clim;
-        fetch<CHECK>(src, cs, row0, col0, rlim, clim, tid, mt_identity{});
+        fetch<CHECK>(src, cs, row0, col0, rlim, clim, tid, mt_identity{}, q, Q);
     }
 
     template <int LD, bool CHECK, typename F>
@@ -337,9 +351,10 @@ struct mt_tile_scalar {
 
     template <bool CHECK, typename F>
     MT_INLINE void fetch(const float* __restrict__ src, unsigned rs, unsigned cs, unsigned row0,
-                         unsigned col0, unsigned rlim, unsigned clim, unsigned tid, F f) {
+                         unsigned col0, unsigned rlim, unsigned clim, unsigned tid, F f, int q = 0, int Q = 1) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
+            if (!mt_in_part(i, PER, q, Q)) continue;
             const unsigned idx = tid + i * NT;
             const unsigned r = idx / COLS, c = idx % COLS;
             const unsigned gr = row0 + r, gc = col0 + c;
@@ -367,9 +382,9 @@ struct mt_tile_scalar {
 
     template <bool CHECK>
     MT_INLINE void fetch_raw(const float* __restrict__ src, unsigned rs, unsigned cs, unsigned row0,
-                             unsigned col0, unsigned rlim, unsigned clim, unsigned tid) {
+                             unsigned col0, unsigned rlim, unsigned clim, unsigned tid, int q = 0, int Q = 1) {
         r0 = row0, c0 = col0, rl = rlim, cl = clim;
-        fetch<CHECK>(src, rs, cs, row0, col0, rlim, clim, tid, mt_identity{});
+        fetch<CHECK>(src, rs, cs, row0, col0, rlim, clim, tid, mt_identity{}, q, Q);
     }
 
     template <int LD, bool CHECK, typename F>
@@ -417,10 +432,11 @@ struct mt_tile_colvec_g : mt_tile_colvec<ROWS, COLS, NT> {
 
     template <bool CHECK, typename G>
     MT_INLINE void fetch_gather(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
-                                unsigned rlim, unsigned clim, unsigned tid, G g) {
+                                unsigned rlim, unsigned clim, unsigned tid, G g, int q = 0, int Q = 1) {
         this->r0 = row0, this->c0 = col0, this->rl = rlim, this->cl = clim;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
+            if (!mt_in_part(i, PER, q, Q)) continue;
             const unsigned idx = tid + i * NT;
             const unsigned r = idx / CV, c = (idx % CV) * 4u;
             const unsigned gr = row0 + r, gc = col0 + c;
@@ -463,10 +479,11 @@ struct mt_tile_rowvec_g : mt_tile_rowvec<ROWS, COLS, NT> {
 
     template <bool CHECK, typename G>
     MT_INLINE void fetch_gather(const float* __restrict__ src, unsigned cs, unsigned row0, unsigned col0,
-                                unsigned rlim, unsigned clim, unsigned tid, G g) {
+                                unsigned rlim, unsigned clim, unsigned tid, G g, int q = 0, int Q = 1) {
         this->r0 = row0, this->c0 = col0, this->rl = rlim, this->cl = clim;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
+            if (!mt_in_part(i, PER, q, Q)) continue;
             const unsigned idx = tid + i * NT;
             const unsigned c = idx / RV, r = (idx % RV) * 4u;
             const unsigned gr = row0 + r, gc = col0 + c;
@@ -507,10 +524,12 @@ struct mt_tile_scalar_g : mt_tile_scalar<ROWS, COLS, NT> {
 
     template <bool CHECK, typename G>
     MT_INLINE void fetch_gather(const float* __restrict__ src, unsigned rs, unsigned cs, unsigned row0,
-                                unsigned col0, unsigned rlim, unsigned clim, unsigned tid, G g) {
+                                unsigned col0, unsigned rlim, unsigned clim, unsigned tid, G g, int q = 0,
+                                int Q = 1) {
         this->r0 = row0, this->c0 = col0, this->rl = rlim, this->cl = clim;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
+            if (!mt_in_part(i, PER, q, Q)) continue;
             const unsigned idx = tid + i * NT;
             const unsigned r = idx / COLS, c = idx % COLS;
             const unsigned gr = row0 + r, gc = col0 + c;
@@ -607,12 +626,13 @@ struct mt_tile_dma {
                   "the tile must split into whole 1 KiB wave loads, the same number per wave");
 
     MT_INLINE void fetch(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
-                         float* lds, unsigned tid) const {
+                         float* lds, unsigned tid, int part = 0, int parts = 1) const {
         const unsigned lane = tid & 63u;
         const unsigned wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const unsigned base = __builtin_amdgcn_readfirstlane(mt_lds_addr(lds));
 #pragma unroll
         for (int q = 0; q < PERW; ++q) {
+            if (!mt_in_part(q, PERW, part, parts)) continue;
             const unsigned inst = wave * PERW + q;
             unsigned r, logical;
             mt_dma_slot<S, SWZ>(inst, lane, r, logical);
@@ -642,9 +662,15 @@ struct mt_tile_dma {
 // same order, so results are identical across layouts.
 // ---------------------------------------------------------------------------
 
-template <int WM, int WN, int TK, int LDA, int LDB, bool ASWZ = false, bool BNM = false>
+// hook(q) runs at the start of each group of 4 k-steps, q = 0 .. TK/8 - 1:
+// the mainloop issues its next chunk's loads there, spread over the MFMAs.
+struct mt_no_hook {
+    MT_INLINE void operator()(int) const {}
+};
+
+template <int WM, int WN, int TK, int LDA, int LDB, bool ASWZ = false, bool BNM = false, typename H = mt_no_hook>
 MT_INLINE void mt_mfma_tile(const float* __restrict__ As, const float* __restrict__ Bs,
-                            mt_f32x16 (&acc)[WM][WN], unsigned lane) {
+                            mt_f32x16 (&acc)[WM][WN], unsigned lane, H hook = H{}) {
     static_assert(TK % 8 == 0, "TK must be a multiple of 8");
     static_assert(LDA % 4 == 0, "LDA must keep 16-byte alignment");
     static_assert(!ASWZ || LDA == TK, "a swizzled A tile is dense");
@@ -665,6 +691,7 @@ MT_INLINE void mt_mfma_tile(const float* __restrict__ As, const float* __restric
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s0 = 0; s0 < HALF; s0 += 4) {
+        hook(s0 / 4);
         const unsigned slot = (lh * HALF + (unsigned)s0) / 4u;  // swizzled tiles: logical 16-byte slot
         mt_f32x4 a[WM];
 #pragma unroll

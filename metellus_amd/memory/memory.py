@@ -185,9 +185,17 @@ class TgLoadFragment:
             )
         return f"{tmpl}<{rows}, {cols}, {self.num_threads}> {self.loader};\nconst auto {self.xform} = {self._lambda()};"
 
-    def render_fetch(self, tid: str = "threadIdx.x", stage: str | None = None) -> str:
+    def render_fetch(self, tid: str = "threadIdx.x", stage: str | None = None, part: str | None = None) -> str:
         """The loads of one tile; ``stage`` is the LDS buffer a direct-to-LDS
-        loader writes (register loaders write at commit and ignore it)."""
+        loader writes (register loaders write at commit and ignore it).
+        ``part`` = "q, Q": only the loads of part q of Q (``mt_in_part``)."""
+        text = self._render_fetch(tid, stage)
+        if part is not None:
+            assert text.endswith(");")
+            text = f"{text[:-2]}, {part});"
+        return text
+
+    def _render_fetch(self, tid: str, stage: str | None) -> str:
         if self.is_dma:
             if stage is None:
                 raise ValueError(f"{self.name}: a direct-to-LDS fetch needs its LDS stage")

@@ -188,6 +188,24 @@ def dma_layouts(tile: TileConfig, srcs_a, srcs_b, pros_a, pros_b, aligned: bool)
 # full-size operands and whose shape needs no bounds checks.
 WIDE_TILES = True
 
+# Matmuls whose prologue gathers full-size operands issue the next k-chunk's
+# register-path loads in LOAD_SPREAD parts spread over the current chunk's
+# MFMAs (MatmulMainloopFragment.spread) instead of in one burst before them:
+# a burst of 12 128-bit loads per lane held every wave in load issue while
+# its MFMAs waited.  Measured on MI355X, C4 (h1*s*h2) @ W3, bit-identical
+# outputs: 2881 -> 2790 us (2 parts) -> 2705 us (4 parts); spreading the
+# direct-to-LDS B loads as well: 2738 us.  Kernels whose loads are all
+# direct-to-LDS, or whose prologue reads only broadcast operands, were
+# slower spread (4096^3 974 -> 996 / 1109 us, C4 X @ W1 2629 -> 2667 /
+# 2728 us, C5 P @ V 276 -> 285 us), so they keep the burst.
+LOAD_SPREAD = 4
+LOAD_SPREAD_DMA = False  # spread direct-to-LDS loads too (measurements only)
+
+
+def load_spread(*prologues: ChainCode | None) -> int:
+    """Spread parts for a mainloop whose A / B prologues are ``prologues``."""
+    return LOAD_SPREAD if any(gathers_full_operands(p) for p in prologues) else 0
+
 
 def gathers(prologue: ChainCode | None) -> bool:
     return GATHER_PROLOGUES and prologue is not None and len(prologue.externals) > 0
@@ -289,6 +307,8 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
                    BarrierFragment("compute_done")),
         K_dim_var="K",
         persistent=persistent is not None,
+        spread=load_spread(pro_a, pro_b),
+        spread_dma=LOAD_SPREAD_DMA,
     )
     store = MatmulEpilogueStoreFragment(config, value_expr=value_expr, check=not aligned)
     fragments = (

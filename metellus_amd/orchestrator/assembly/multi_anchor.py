@@ -142,6 +142,8 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
                 ),
                 K_dim_var="K",
                 persistent=persistent is not None,
+                spread=_mm.load_spread(*tf_b),
+                spread_dma=_mm.LOAD_SPREAD_DMA,
             )
         ]
     else:
@@ -160,6 +162,8 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
                         BarrierFragment(f"compute{i}_done"),
                     ),
                     K_dim_var=kvars[i],
+                    spread=_mm.load_spread(tf_a[i], tf_b[i]),
+                    spread_dma=_mm.LOAD_SPREAD_DMA,
                 )
             )
 

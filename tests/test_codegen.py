@@ -2,6 +2,8 @@
 generated source (no GPU): where matmul prologues are applied, and how
 batched kernels address their per-program buffers."""
 
+import re
+
 import pytest
 
 from metellus_amd.api import compile_program
@@ -133,24 +135,43 @@ def test_persistent_switch_off_restores_classic_grid(monkeypatch):
     assert g.grid[2] == 1 and g.grid[0] * g.grid[1] > 2
 
 
-@pytest.mark.parametrize(
-    "case",
-    [
-        lambda: gpu_cases.plain_matmul(512, 512, 512),
-        lambda: gpu_cases.attention_head(512, 128),
-        lambda: gpu_cases.mlp_block(256, 256, 512),
-    ],
-    ids=["gemm", "attention", "mlp"],
-)
-def test_direct_to_lds_kernels_wait_for_every_memory_operation(case):
+WAIT_CASES = {
+    "gemm": (lambda: gpu_cases.plain_matmul(512, 512, 512), None),
+    "attention": (lambda: gpu_cases.attention_head(512, 128), None),
+    "mlp": (lambda: gpu_cases.mlp_block(256, 256, 512), None),
+    "gemm persistent": (lambda: gpu_cases.plain_matmul(1024, 256, 1024), (4, False, "mt_t += gridDim.x")),
+    "gemm stream-K": (lambda: gpu_cases.plain_matmul(1024, 256, 1024), (5, True, "mt_sk.init(")),
+    "mlp stream-K": (lambda: gpu_cases.mlp_block(512, 256, 1024), (3, True, "mt_sk.init(")),
+    "diamond stream-K": (lambda: gpu_cases.mlp_block(512, 256, 640, diamond=True), (6, True, "mt_sk.init(")),
+}
+
+
+@pytest.mark.parametrize("name", sorted(WAIT_CASES))
+def test_direct_to_lds_kernels_wait_for_every_memory_operation(name, monkeypatch):
     # A direct-to-LDS chunk shares the vector-memory counter with the
     # epilogue's stores, and the two do not retire in issue order, so the
     # only safe wait before the barrier that publishes a chunk is a full
     # s_waitcnt(0): a partial count can pass with the chunk still in flight.
-    dma = [g for g in compile_program(case()) if "mt_tile_dma<" in g.kernel.source.split('extern "C"')[-1]]
+    # Checked in every form a wait can take in the kernel's whole source
+    # (the device library included): the builtin and inline asm.
+    from metellus_amd.compute.matmul import config
+
+    build, loop = WAIT_CASES[name]
+    if loop is not None:
+        capacity, stream_k, marker = loop
+        monkeypatch.setattr(config, "PERSISTENT", True)
+        monkeypatch.setattr(config, "PERSISTENT_CAPACITY", capacity)
+        monkeypatch.setattr(config, "STREAM_K", stream_k)
+    dma = [g for g in compile_program(build()) if "mt_tile_dma<" in g.kernel.source.split('extern "C"')[-1]]
     assert dma
+    if loop is not None:
+        assert any(marker in g.kernel.source.split('extern "C"')[-1] for g in dma), name
     for g in dma:
-        body = g.kernel.source.split('extern "C"')[-1]
-        waits = body.split("__builtin_amdgcn_s_waitcnt(")[1:]
-        assert waits, g.kernel.function_name
-        assert all(w.startswith("0)") for w in waits), g.kernel.function_name
+        src = g.kernel.source
+        builtin = re.findall(r"__builtin_amdgcn_s_waitcnt\(([^)]*)\)", src)
+        assert builtin and all(w.strip() == "0" for w in builtin), (g.kernel.function_name, builtin)
+        asm_text = " ".join(re.findall(r'asm\s*(?:volatile\s*)?\(\s*((?:"[^"]*"\s*)+)', src))
+        asm_waits = re.findall(r"s_waitcnt[^\\\"]*", asm_text)
+        assert all(re.fullmatch(r"s_waitcnt\s+(0|vmcnt\(0\)(\s+lgkmcnt\(0\))?)\s*", w) for w in asm_waits), (
+            g.kernel.function_name, asm_waits)
+        assert hip_backend.compile_only(src) > 0
