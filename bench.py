@@ -30,7 +30,7 @@ torch on the CPU -- both pinned to the same thread count; ``per_config``
 does the same for every other configuration.  ``end_to_end``: ``api.run``
 wall times for C2 and C3 (host transfers included).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|fragments|ceilings]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|copy|fragments|ceilings]
        [--no-extra] [--no-cpu] [--no-flush] [--calibrate-copy]
 """
 
@@ -88,6 +88,18 @@ def _c5(head=0):
     from tests.gpu_cases import attention_head
 
     return attention_head(2048, 128, seed=4, head=head, heads=32)
+
+
+def _copy():
+    """The shape-copy path (a reshape that cannot be a view): a transposed
+    4096x4096 fp32 view flattened -- 64 MiB read, 64 MiB written."""
+    from metellus_amd.orchestrator import Operations
+
+    ops = Operations()
+    ops.from_numpy(np.random.default_rng(5).standard_normal((4096, 4096)).astype(np.float32), "X")
+    ops.transpose("X", out="Xt")
+    ops.reshape("Xt", (4096 * 4096,), out="Y")
+    return ops
 
 
 # ---------------------------------------------------------------------------
@@ -875,6 +887,8 @@ def main() -> int:
             todo.append(("C4 MLP diamond", lambda: _c4(True)))
         if only in (None, "c5"):
             todo.append(("C5 attention, 32 heads batched", lambda: [_c5(h) for h in range(32)]))
+        if only in (None, "copy"):
+            todo.append(("shape copy: transposed 4096x4096 view", _copy))
         for label, make in todo:
             log(f"[bench] {label}: preparing")
             made = make()

@@ -118,9 +118,11 @@ class ChainCode:
     seeds: tuple[str, ...]
     name: str
     externals: list[External] = field(default_factory=list)
-    # Divisions feeding a matmul (operand prologues, register epilogues,
-    # multi-anchor merges) use mt_div_fast: within 2 ulp of the IEEE
-    # quotient, which the matmul bar (1e-4 sqrt(K)) leaves no trace of.
+    # Divisions feeding a matmul (operand prologues) use mt_div_fast: within
+    # 2 ulp of the IEEE quotient, which the matmul bar (1e-4 sqrt(K)) leaves
+    # no trace of.  Epilogues and multi-anchor merges produce the kernel's
+    # output and keep IEEE division, so a fused chain rounds exactly like
+    # the same chain in its own elementwise kernel.
     fast_div: bool = False
 
     def __post_init__(self) -> None:

@@ -91,6 +91,11 @@ class MatmulTileMappingFragment:
     name: str = "tile_mapping"
     kind: str = "setup"
 
+    @property
+    def opens_tile_loop(self) -> bool:
+        """LDS lifetime analysis: fragments up to the loop end run repeatedly."""
+        return self.persistent is not None
+
     def render(self, ctx: CodegenContext) -> str:
         p = self.persistent
         if p is None:
@@ -230,6 +235,7 @@ class PersistentLoopEndFragment:
 
     name: str = "persistent_loop_end"
     kind: str = "setup"
+    closes_tile_loop: bool = True
 
     def render(self, ctx: CodegenContext) -> str:
         return "}  // persistent tile loop"

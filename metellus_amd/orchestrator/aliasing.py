@@ -55,8 +55,31 @@ def _walk_accesses(fragment: object) -> Iterable[TgmemAccess]:
         yield from _walk_accesses(sub)
 
 
+def _tile_loops(kernel: Kernel) -> list[tuple[int, int]]:
+    """(open, close) top-level indices of the persistent tile loops: a
+    fragment with ``opens_tile_loop`` true up to the next one with
+    ``closes_tile_loop``."""
+    spans, start = [], None
+    for idx, frag in enumerate(kernel.fragments):
+        if getattr(frag, "opens_tile_loop", False):
+            start = idx
+        elif getattr(frag, "closes_tile_loop", False) and start is not None:
+            spans.append((start, idx))
+            start = None
+    if start is not None:
+        raise ValueError("a persistent tile loop is opened but never closed")
+    return spans
+
+
 def compute_lifetimes(kernel: Kernel) -> tuple[TgmemLifetime, ...]:
-    """One lifetime per LDS name, in first-touch order."""
+    """One lifetime per LDS name, in first-touch order.
+
+    The fragments are straight-line code except inside a persistent tile
+    loop, where the last k-chunk of an item already loads the next item's
+    first chunk into the operand tiles (directly into LDS, possibly still in
+    flight) while the item's epilogue runs: every name touched inside such a
+    loop lives for the whole loop, so nothing touched there shares a slot
+    with anything else touched there."""
     first: dict[str, int] = {}
     last: dict[str, int] = {}
     biggest: dict[str, TgmemAccess] = {}
@@ -68,6 +91,10 @@ def compute_lifetimes(kernel: Kernel) -> tuple[TgmemLifetime, ...]:
             elif acc.size_floats > biggest[acc.name].size_floats:
                 biggest[acc.name] = acc
             last[acc.name] = idx
+    for lo, hi in _tile_loops(kernel):
+        for n in first:
+            if first[n] <= hi and last[n] >= lo:
+                first[n], last[n] = min(first[n], lo), max(last[n], hi)
     return tuple(
         TgmemLifetime(
             name=n,

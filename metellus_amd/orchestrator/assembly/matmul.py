@@ -140,8 +140,9 @@ def operand_load(
 # cost one register per loader slot).
 GATHER_PROLOGUES = True
 GATHER_TILE_K = 16
-# Divisions inside matmul prologues / epilogues / merges use mt_div_fast
-# (a refined reciprocal times the numerator, within 2 ulp of IEEE division).
+# Divisions inside matmul operand prologues use mt_div_fast (a refined
+# reciprocal times the numerator, within 2 ulp of IEEE division); register
+# epilogues and multi-anchor merges keep IEEE division.
 FAST_DIV = True
 
 
@@ -258,7 +259,7 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         helpers.append(pro_b.helper())
     value_expr = None
     if decision.epilogue:
-        epi = ChainCode(decision.epilogue, (anchor.out.name,), "epilogue", fast_div=FAST_DIV)
+        epi = ChainCode(decision.epilogue, (anchor.out.name,), "epilogue")  # IEEE division: the output
         epi.register_extras(extras, base)
         helpers.append(epi.helper())
         value_expr = epi.scalar_call(["{a0}"], "row", "col")

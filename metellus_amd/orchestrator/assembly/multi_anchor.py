@@ -91,7 +91,7 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
 
     tf_a = tuple(prologue(pro_a[i], src_a[i], f"prologue_a{i}") for i in range(2))
     tf_b = tuple(prologue(pro_b[i], src_b[i], f"prologue_b{i}") for i in range(2))
-    merge_code = ChainCode((merge,), (a0.out.name, a1.out.name), "merge", fast_div=_mm.FAST_DIV)
+    merge_code = ChainCode((merge,), (a0.out.name, a1.out.name), "merge")  # IEEE division: the output
     helpers.append(merge_code.helper())
     value_expr = merge_code.call(["{a0}", "{a1}"], [])
 

@@ -5,8 +5,10 @@ Plan, in order:
 
 1. ``FromNumpy`` for every uploaded input (validated: every external input
    buffer has an upload and every upload is a program input);
-2. ``Allocate`` for each non-input buffer at first use, and each kernel
-   (to render its source off the dispatch path);
+2. ``Allocate`` for every non-input buffer, all of them before the first
+   ``Dispatch`` and in first-use order (as the reference does), so the
+   peak device footprint is the sum of the materialised buffers; each
+   kernel is rendered here too, off the dispatch path;
 3. one ``Dispatch`` per group; after it, every buffer whose last use it was
    is downloaded -- each view of it first (host gather through the view's
    strides), then the owner itself if it is a named tensor (which ends the

@@ -111,3 +111,61 @@ def test_unparseable_declaration_rejected():
     k = Kernel(g.kernel.fragments, bad_ctx)
     with pytest.raises(ValueError, match="cannot parse"):
         apply_alias_map(k, compute_alias_map(compute_lifetimes(k)))
+
+
+def _with_c_tile(persistent_capacity, monkeypatch):
+    """An assembled matmul with a C tile staged through LDS after its
+    mainloop (MatmulAccumToTgFragment -> barrier -> MatmulTgToDevFragment),
+    as a hand-composed kernel would add it."""
+    import dataclasses
+
+    from compute.fragments import BarrierFragment, lds_decl
+    from compute.matmul import config
+    from compute.matmul.matmul import (
+        MatmulAccumToTgFragment,
+        MatmulEpilogueStoreFragment,
+        MatmulMainloopFragment,
+        MatmulTgToDevFragment,
+    )
+    from runtime import Kernel
+
+    monkeypatch.setattr(config, "PERSISTENT", True)
+    monkeypatch.setattr(config, "PERSISTENT_CAPACITY", persistent_capacity)
+    monkeypatch.setattr(config, "STREAM_K", False)
+    ops = Operations()
+    ops.input("A", shape=(512, 256))
+    ops.input("B", shape=(256, 512))
+    ops.matmul(a="A", b="B", out="C")
+    g = assemble(fuse(ops.build())[0])
+    frags = list(g.kernel.fragments)
+    i = next(k for k, f in enumerate(frags) if isinstance(f, MatmulEpilogueStoreFragment))
+    cfg = next(f for f in frags if isinstance(f, MatmulMainloopFragment)).fragments[3].config
+    frags[i : i + 1] = [MatmulAccumToTgFragment(cfg), BarrierFragment("c_ready"), MatmulTgToDevFragment(cfg)]
+    t = cfg.tile
+    decls = (*g.kernel.ctx.threadgroup_decls, lds_decl("C_tile", (t.tile_M, t.tile_N + t.c_pad)))
+    return Kernel(tuple(frags), dataclasses.replace(g.kernel.ctx, threadgroup_decls=decls))
+
+
+def test_persistent_loop_keeps_post_mainloop_tenants_apart(monkeypatch):
+    # In a persistent tile loop the mainloop's last chunk loads the next
+    # tile's first chunk into A_tile/B_tile (directly into LDS) while the
+    # epilogue runs, so a C tile born after the mainloop must not reuse
+    # their storage.
+    k = _with_c_tile(2, monkeypatch)
+    assert any(getattr(f, "opens_tile_loop", False) for f in k.fragments)
+    plan = compute_alias_map(compute_lifetimes(k))
+    slot_of = plan.name_to_slot
+    assert slot_of["C_tile"] not in (slot_of["A_tile"], slot_of["B_tile"])
+    assert all(len(s.tenants) == 1 for s in plan.slots)
+    lts = {lt.name: lt for lt in compute_lifetimes(k)}
+    end = next(i for i, f in enumerate(k.fragments) if getattr(f, "closes_tile_loop", False))
+    assert lts["A_tile"].death == end and lts["C_tile"].death == end
+
+
+def test_one_tile_per_workgroup_lets_the_c_tile_reuse_operand_storage(monkeypatch):
+    # the same kernel without the loop: straight-line code, so the C tile
+    # (born after the operands' last use) joins an operand slot
+    k = _with_c_tile(10_000, monkeypatch)
+    assert not any(getattr(f, "opens_tile_loop", False) for f in k.fragments)
+    plan = compute_alias_map(compute_lifetimes(k))
+    assert any("C_tile" in s.tenants and len(s.tenants) > 1 for s in plan.slots)

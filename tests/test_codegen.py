@@ -6,7 +6,10 @@ import re
 
 import pytest
 
+import numpy as np
+
 from metellus_amd.api import compile_program
+from metellus_amd.orchestrator import Operations
 from metellus_amd.runtime import hip_backend
 from tests import gpu_cases
 
@@ -175,3 +178,22 @@ def test_direct_to_lds_kernels_wait_for_every_memory_operation(name, monkeypatch
         assert all(re.fullmatch(r"s_waitcnt\s+(0|vmcnt\(0\)(\s+lgkmcnt\(0\))?)\s*", w) for w in asm_waits), (
             g.kernel.function_name, asm_waits)
         assert hip_backend.compile_only(src) > 0
+
+
+def test_epilogue_and_merge_division_stay_ieee():
+    # (A @ B) / d and a diamond merged by division produce the output: IEEE
+    ops = gpu_cases.plain_matmul(256, 128, 256)
+    ops.from_numpy(np.ones(256, np.float32), "d")
+    ops.reshape("d", (256, 1), out="dc")
+    ops.elementwise("div", out="Y", operands=("C", "dc"), y_broadcast="col")
+    (g,) = compile_program(ops)
+    assert "mt_div_fast(" not in "".join(g.kernel.ctx.helpers) and "/" in "".join(g.kernel.ctx.helpers)
+    ops = Operations()
+    for n, shape in (("X", (256, 128)), ("W1", (128, 256)), ("W2", (128, 256))):
+        ops.input(n, shape)
+    ops.matmul(a="X", b="W1", out="h1")
+    ops.matmul(a="X", b="W2", out="h2")
+    ops.elementwise("div", out="z", operands=("h1", "h2"))
+    (g,) = compile_program(ops)
+    assert g.kernel.function_name.startswith("multi_anchor")
+    assert "mt_div_fast(" not in "".join(g.kernel.ctx.helpers)

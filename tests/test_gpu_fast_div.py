@@ -75,3 +75,44 @@ def test_fast_division_matches_ieee():
     np.testing.assert_array_equal(fast[zero].view(np.uint32), ieee[zero].view(np.uint32))
     sub = finite & ~normal
     assert np.all(np.abs(fast[sub].astype(np.float64) - ieee[sub]) <= 2.0 ** -148)
+
+
+@pytest.mark.parametrize("op", ["div", "recip"])
+def test_fused_epilogue_division_rounds_like_the_unfused_chain(op):
+    """A division fused into a matmul's register epilogue is IEEE division,
+    so ``(A @ B) / d`` and ``recip(A @ B)`` fused give exactly what the same
+    op gives in its own elementwise kernel on the matmul's output."""
+    from metellus_amd.api import run
+    from metellus_amd.orchestrator import Operations
+
+    rng = np.random.default_rng(37)
+    a = rng.standard_normal((256, 192)).astype(np.float32)
+    b = rng.standard_normal((192, 320)).astype(np.float32)
+    d = rng.uniform(0.3, 3.0, 256).astype(np.float32)
+
+    def tail(ops, src):
+        if op == "div":
+            ops.from_numpy(d, "d")
+            ops.reshape("d", (256, 1), out="dc")
+            ops.elementwise("div", out="Y", operands=(src, "dc"), y_broadcast="col")
+        else:
+            ops.elementwise("recip", out="Y", operands=(src,))
+
+    fused = Operations()
+    fused.from_numpy(a, "A")
+    fused.from_numpy(b, "B")
+    fused.matmul(a="A", b="B", out="C")
+    tail(fused, "C")
+    res = run(fused, outputs=("Y",))
+    assert len(res.groups) == 1, [g.strategy for g in res.groups]
+    assert "mt_div_fast(" not in "".join(res.groups[0].kernel.ctx.helpers)
+    mm = Operations()
+    mm.from_numpy(a, "A")
+    mm.from_numpy(b, "B")
+    mm.matmul(a="A", b="B", out="C")
+    c = run(mm).env["C"]
+    ew = Operations()
+    ew.from_numpy(c, "Cm")
+    tail(ew, "Cm")
+    unfused = run(ew).env["Y"]
+    np.testing.assert_array_equal(res.env["Y"], unfused)

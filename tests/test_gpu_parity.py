@@ -301,7 +301,14 @@ def test_attention_head(S, Dh):
 # ---------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("shape,new", [((8, 16), (128,)), ((8, 16), (32, 4)), ((10, 13), (130,)), ((32, 32), (1024,))])
+@pytest.mark.parametrize(
+    "shape,new",
+    [
+        ((8, 16), (128,)), ((8, 16), (32, 4)), ((10, 13), (130,)), ((32, 32), (1024,)),
+        # LDS-tiled transpose copy: ragged 64x64 tiles in both axes, and a large one
+        ((65, 130), (8450,)), ((300, 257), (514, 150)), ((4096, 1024), (4194304,)),
+    ],
+)
 def test_shape_copy_exact(shape, new):
     rng = np.random.default_rng(0)
     x = rng.standard_normal(shape).astype(np.float32)

@@ -10,6 +10,8 @@ from orchestrator.assembly import assemble
 from orchestrator.fusion import fuse
 from orchestrator.kernel_group import FusionStrategy
 
+from metellus_amd.runtime import hip_backend
+
 
 def test_tensor_view_basics():
     assert Tensor("x", (8, 16)).buffer_key == "x"
@@ -158,9 +160,27 @@ def test_shape_kernel_strides_and_launch():
     ops.reshape("Xt", (32,), out="Y")
     g = assemble(fuse(ops.build())[0])
     src = g.kernel.source
-    assert "in_row * 1u + in_col * 8u" in src
-    assert "global_idx / 4u" in src and "global_idx % 4u" in src
-    assert g.bindings == ("X", "Y")
+    # a transposed view (row stride 1, column stride 8): LDS-tiled transpose
+    # reading the owner's buffer along its contiguous axis, 128-bit wide
+    assert "mt_ld4(g_X + (size_t)(j0 + jj) * 8u + i0 + l4)" in src
+    assert "__shared__ alignas(16) float copy_tile[64][65];" in src
+    assert g.bindings == ("X", "Y") and g.dims == (32,)
+    assert hip_backend.compile_only(src) > 0
+    ops = Operations()  # 13 x 10 transposed view: scalar tiles
+    ops.input("X", shape=(10, 13))
+    ops.transpose("X", out="Xt")
+    ops.reshape("Xt", (130,), out="Y")
+    src = assemble(fuse(ops.build())[0]).kernel.source
+    assert "g_X[(size_t)j * 13u + i]" in src and "mt_ld4" not in src.split('extern "C"')[1]
+    assert hip_backend.compile_only(src) > 0
+    # any other strides: one lane per element through the strides
+    from compute.copy.copy import StridedCopyFragment
+    from compute.fragments import CodegenContext
+
+    frag = StridedCopyFragment("g_X", "g_Y", 12, 4, 3, input_rows=2)
+    text = frag.render(CodegenContext(function_name="k", buffers=(), dims=("N",), tg_x=256, tg_y=1))
+    assert "(size_t)in_row * 12u + (size_t)in_col * 4u" in text
+    assert "global_idx / 3u" in text and "global_idx % 3u" in text and "const unsigned global_idx" in text
     ops = Operations()
     ops.input("X", shape=(10, 13))
     ops.transpose("X", out="Xt")
