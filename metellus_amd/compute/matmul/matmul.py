@@ -460,13 +460,16 @@ class MatmulMainloopFragment:
         the MFMAs, or the spread ones in ``mt_hook``'s parts."""
 
         def guarded(lds, part, pad):
-            fetch = [ld.render_fetch(stage="cur ^ 1u", part=part) for ld in lds]
+            # the next chunk of this tile (k-invariant gathers kept), or the
+            # first chunk of the next item's tile (gathered afresh)
+            same = [ld.render_fetch(stage="cur ^ 1u", part=part, reuse=True) for ld in lds]
             lines = ["if (more) {", f"    const unsigned k_chunk = (kt + 1u) * {self.tile_K}u;",
-                     *[f"    {x}" for x in fetch]]
+                     *[f"    {x}" for x in same]]
             if persistent:
+                first = [ld.render_fetch(stage="cur ^ 1u", part=part) for ld in lds]
                 lines += ["} else if (mt_has_next) {", "    const unsigned tile_m0 = mt_next_m0;",
                           "    const unsigned tile_n0 = mt_next_n0;",
-                          f"    const unsigned k_chunk = mt_next_kb * {self.tile_K}u;", *[f"    {x}" for x in fetch]]
+                          f"    const unsigned k_chunk = mt_next_kb * {self.tile_K}u;", *[f"    {x}" for x in first]]
             return [pad + x for x in (*lines, "}")]
 
         early = [ld for ld in loads if not (spread and self._is_spread(ld))]

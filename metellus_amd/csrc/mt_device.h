@@ -450,6 +450,18 @@ struct mt_tile_colvec_g : mt_tile_colvec<ROWS, COLS, NT> {
         }
     }
 
+    // SLOT gathers are constant along the loaded rows' k axis, so the next
+    // chunk of the same tile needs the same operands: fetch_keep loads the
+    // tile alone and keeps ex (and the work derived from it, such as a
+    // divisor's reciprocal, stays loop-invariant for the compiler).
+    template <bool CHECK>
+    MT_INLINE void fetch_keep(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
+                              unsigned rlim, unsigned clim, unsigned tid, int q = 0, int Q = 1) {
+        static_assert(SLOT, "only per-slot gathers are invariant along k");
+        this->r0 = row0, this->c0 = col0, this->rl = rlim, this->cl = clim;
+        Base::template fetch<CHECK>(src, rs, row0, col0, rlim, clim, tid, mt_identity{}, q, Q);
+    }
+
     template <int LD, bool CHECK, typename A>
     MT_INLINE void commit_apply(float* lds, unsigned tid, A a) {
 #pragma unroll
@@ -495,6 +507,14 @@ struct mt_tile_rowvec_g : mt_tile_rowvec<ROWS, COLS, NT> {
             }
             this->v[i] = x;
         }
+    }
+
+    template <bool CHECK>
+    MT_INLINE void fetch_keep(const float* __restrict__ src, unsigned cs, unsigned row0, unsigned col0,
+                              unsigned rlim, unsigned clim, unsigned tid, int q = 0, int Q = 1) {
+        static_assert(SLOT, "only per-slot gathers are invariant along k");
+        this->r0 = row0, this->c0 = col0, this->rl = rlim, this->cl = clim;
+        Base::template fetch<CHECK>(src, cs, row0, col0, rlim, clim, tid, mt_identity{}, q, Q);
     }
 
     template <int LD, bool CHECK, typename A>

@@ -96,6 +96,11 @@ class TgLoadFragment:
     # column broadcast for "colvec", a row broadcast for "rowvec"): gather
     # them once per 128-bit slot.
     gather_per_slot: bool = False
+    # The per-slot operands are also constant along the matmul's k axis (the
+    # loader walks k along its vector axis), so every k-chunk of one output
+    # tile needs the same ones: they are gathered with a tile's first chunk
+    # and kept for the rest (``render_fetch(reuse=True)``: fetch_keep).
+    gather_invariant: bool = False
     # mode "dma": direct-to-LDS loads (mt_tile_dma) of a row-major source
     # (row stride src_row_stride, unit column stride, every element in
     # bounds, no transform) into a dense tile of tile_shape; the fetch
@@ -177,6 +182,8 @@ class TgLoadFragment:
                 raise ValueError(f"{self.name}: gather/apply needs a proven load mode and an apply lambda")
             if self.gather_per_slot and mode not in ("colvec", "rowvec"):
                 raise ValueError(f"{self.name}: per-slot gathers need a vectorised load mode")
+            if self.gather_invariant and not self.gather_per_slot:
+                raise ValueError(f"{self.name}: k-invariant gathers are per-slot gathers")
             slot = ", true" if self.gather_per_slot else ""
             return (
                 f"{tmpl}_g<{rows}, {cols}, {self.num_threads}, {self.n_gathered}{slot}> {self.loader};\n"
@@ -185,11 +192,25 @@ class TgLoadFragment:
             )
         return f"{tmpl}<{rows}, {cols}, {self.num_threads}> {self.loader};\nconst auto {self.xform} = {self._lambda()};"
 
-    def render_fetch(self, tid: str = "threadIdx.x", stage: str | None = None, part: str | None = None) -> str:
+    def render_fetch(
+        self, tid: str = "threadIdx.x", stage: str | None = None, part: str | None = None, reuse: bool = False
+    ) -> str:
         """The loads of one tile; ``stage`` is the LDS buffer a direct-to-LDS
         loader writes (register loaders write at commit and ignore it).
-        ``part`` = "q, Q": only the loads of part q of Q (``mt_in_part``)."""
-        text = self._render_fetch(tid, stage)
+        ``part`` = "q, Q": only the loads of part q of Q (``mt_in_part``).
+        ``reuse``: a later chunk of the same output tile -- a loader with
+        k-invariant gathered operands keeps them (``fetch_keep``)."""
+        if reuse and self.gathering and self.gather_invariant:
+            check = "true" if self.check else "false"
+            rlim = self.row_limit if self.row_limit is not None else "0xffffffffu"
+            clim = self.col_limit if self.col_limit is not None else "0xffffffffu"
+            strides = self.src_row_stride if self.resolved_mode() == "colvec" else self.src_col_stride
+            text = (
+                f"{self.loader}.template fetch_keep<{check}>({self.src_name}, {strides}, {self.row_start}, "
+                f"{self.col_start}, {rlim}, {clim}, {tid});"
+            )
+        else:
+            text = self._render_fetch(tid, stage)
         if part is not None:
             assert text.endswith(");")
             text = f"{text[:-2]}, {part});"

@@ -107,6 +107,11 @@ def operand_load(
     # one gather per 128-bit slot when the operands do not change along it
     along = {"colvec": "col", "rowvec": "row"}.get(mode)
     per_slot = gather and along is not None and along not in prologue.external_axes()
+    # ... and when that vector axis is k (A along its columns, B along its
+    # rows), a tile's k-chunks all need the same operands: gathered once per
+    # tile (and a divisor's reciprocal becomes loop-invariant).  Measured on
+    # MI355X, C5 O = (e / s1) @ V, bit-identical: 277.1 -> 272.1 us.
+    invariant = per_slot and ((side == "a" and mode == "colvec") or (side == "b" and mode == "rowvec"))
     return TgLoadFragment(
         name=name,
         src_name=param_name(src.buffer_key),
@@ -128,6 +133,7 @@ def operand_load(
         apply_lambda=prologue.apply_lambda() if gather else None,
         n_gathered=len(prologue.externals) if gather else 0,
         gather_per_slot=per_slot,
+        gather_invariant=invariant and GATHER_ONCE_PER_TILE,
     )
 
 
@@ -140,6 +146,7 @@ def operand_load(
 # cost one register per loader slot).
 GATHER_PROLOGUES = True
 GATHER_TILE_K = 16
+GATHER_ONCE_PER_TILE = True  # k-invariant per-slot operands gathered with a tile's first chunk only
 # Divisions inside matmul operand prologues use mt_div_fast (a refined
 # reciprocal times the numerator, within 2 ulp of IEEE division); register
 # epilogues and multi-anchor merges keep IEEE division.

@@ -197,3 +197,26 @@ def test_epilogue_and_merge_division_stay_ieee():
     (g,) = compile_program(ops)
     assert g.kernel.function_name.startswith("multi_anchor")
     assert "mt_div_fast(" not in "".join(g.kernel.ctx.helpers)
+
+
+def test_k_invariant_gathers_are_loaded_once_per_tile(monkeypatch):
+    # P @ V with P = e / s1: s1 depends on the row only, so the A loader
+    # gathers it with a tile's first chunk and keeps it for the later ones;
+    # on the persistent path the next tile's first chunk gathers afresh
+    from metellus_amd.compute.matmul import config
+
+    g = _by_name(compile_program(gpu_cases.attention_head(512, 64)))["matmul_O_fused"]
+    loop = g.kernel.source.split("for (unsigned kt = 0; kt < n_chunks; ++kt)")[1]
+    assert "ld_A_tile.template fetch_keep<false>(g_e, " in loop and "fetch_gather" not in loop
+    assert hip_backend.compile_only(g.kernel.source) > 0
+    monkeypatch.setattr(config, "PERSISTENT", True)
+    monkeypatch.setattr(config, "PERSISTENT_CAPACITY", 2)
+    monkeypatch.setattr(config, "STREAM_K", False)
+    g = _by_name(compile_program(gpu_cases.attention_head(512, 64)))["matmul_O_fused"]
+    loop = g.kernel.source.split("for (unsigned kt = mt_kb; kt < mt_ke; ++kt)")[1]
+    more, nxt = loop.split("} else if (mt_has_next) {")
+    assert "fetch_keep<" in more and "fetch_gather<" in nxt.split("}")[0]
+    assert hip_backend.compile_only(g.kernel.source) > 0
+    # full-size gathered operands change with k: gathered with every chunk
+    w3 = _by_name(compile_program(gpu_cases.mlp_block(256, 256, 512)))["matmul_out_fused"]
+    assert "fetch_keep" not in w3.kernel.source.split('extern "C"')[1]
