@@ -30,7 +30,7 @@ torch on the CPU -- both pinned to the same thread count; ``per_config``
 does the same for every other configuration.  ``end_to_end``: ``api.run``
 wall times for C2 and C3 (host transfers included).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|copy|fragments|ceilings]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|gemm|c5|copy|fragments|ceilings|sweep]
        [--no-extra] [--no-cpu] [--no-flush] [--calibrate-copy]
 """
 
@@ -581,6 +581,121 @@ def ceiling_benches(steps: int, flusher) -> list[dict]:
     return out
 
 
+# A read-only stream of a different design from the framework's row
+# reductions (one wave per row): workgroup g reads the g-th contiguous
+# chunk of n / grid float4s, its lanes on adjacent 16-byte slots with four
+# 128-bit nontemporal loads in flight each, then each wave writes one
+# partial sum.  Its time is a ceiling for reads on the box that does not
+# depend on the generated kernels (the best of the designs measured:
+# grid-stride walks with 4-16 loads in flight ran at 5.3-6.8 TB/s).
+READ_CEILING_SRC = r"""
+typedef float rc_f4 __attribute__((ext_vector_type(4)));
+struct rc_dims { unsigned int v[16]; };
+extern "C" __global__ void __launch_bounds__(256)
+read_ceiling(const rc_f4* __restrict__ x, float* __restrict__ out, const rc_dims dims) {
+    const unsigned per = dims.v[0] / gridDim.x;
+    const rc_f4* p = x + (size_t)blockIdx.x * per;
+    rc_f4 a = {0.f, 0.f, 0.f, 0.f}, b = a, c = a, d = a;
+    unsigned j = threadIdx.x;
+    for (; j + 768u < per; j += 1024u) {
+        a += __builtin_nontemporal_load(p + j);
+        b += __builtin_nontemporal_load(p + j + 256u);
+        c += __builtin_nontemporal_load(p + j + 512u);
+        d += __builtin_nontemporal_load(p + j + 768u);
+    }
+    for (; j < per; j += 256u) a += __builtin_nontemporal_load(p + j);
+    a += b + c + d;
+    float s = (a.x + a.y) + (a.z + a.w);
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((threadIdx.x & 63u) == 0u) out[blockIdx.x * 4u + (threadIdx.x >> 6)] = s;
+}
+"""
+READ_CEILING_GRIDS = (2048, 8192, 32768)  # workgroups of 256 lanes; each divides the float4 count
+SWEEP_SCALES = (1, 2, 4)
+
+
+def read_ceiling(buf, nbytes: int, steps: int, flusher, label: str) -> list[dict]:
+    """Time ``read_ceiling`` over the first ``nbytes`` of ``buf`` at each of
+    ``READ_CEILING_GRIDS``; work = bytes read + the partial sums written."""
+    from metellus_amd.runtime import hip_backend
+    from metellus_amd.runtime.buffer import Buffer
+
+    n4 = nbytes // 16
+    if nbytes % 16 or n4 >= 2**32 or nbytes > buf.nbytes or any(n4 % g for g in READ_CEILING_GRIDS):
+        raise ValueError(f"read_ceiling: {nbytes} bytes do not split into the kernel's float4 chunks or fit the buffer")
+    kernel = hip_backend.compile_kernel(READ_CEILING_SRC, "read_ceiling")
+    out = Buffer(4 * 4 * max(READ_CEILING_GRIDS))
+    recs = []
+    for grid in READ_CEILING_GRIDS:
+        def launch(timed, grid=grid):
+            return hip_backend.launch(kernel, [buf, out], [nbytes // 16], 2, (grid, 1, 1), (256, 1, 1), timed=timed)
+        warm_up(launch, flusher, 2)
+        hip_backend.synchronize()
+        ms = []
+        for _ in range(steps):
+            if flusher is not None:
+                flusher.flush()
+            ms.append(launch(True))
+        work = float(nbytes + 4 * 4 * grid)
+        mean = float(np.mean(ms))
+        achieved = work / (mean * 1e-3) / 1e9
+        recs.append({"kernel": "read_ceiling", "config": f"{label} grid {grid}", "grid": [grid, 1, 1],
+                     "threads": [256, 1, 1], "ms_mean": round(mean, 5), "ms_min": round(float(np.min(ms)), 5),
+                     "ms_median": round(float(np.median(ms)), 5), "bound": "hbm", "work": work,
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4)})
+        log(f"[bench] {label} read_ceiling grid {grid}: {mean:.4f} ms  {achieved:.1f} GB/s "
+            f"({100 * achieved / HBM_PEAK_GBS:.1f}%)")
+    out.release()
+    return recs
+
+
+def fit_sweep(records: list[dict]) -> list[dict]:
+    """Least-squares ``t = t0 + bytes / rate`` per kernel over the sweep's
+    sizes: ``rate`` is the steady-state stream rate, ``t0`` the fixed cost
+    (launch ramp, tail) that the smaller sizes cannot amortise."""
+    groups: dict[str, list[tuple[float, float]]] = {}
+    for r in records:
+        fam = r["config"].split(" x", 1)[0] + " / " + r["kernel"] + (
+            " " + r["config"].rsplit(" ", 2)[-2] + " " + r["config"].rsplit(" ", 1)[-1]
+            if r["kernel"] == "read_ceiling" else "")
+        groups.setdefault(fam, []).append((r["work"], r["ms_mean"] * 1e-3))
+    fits = []
+    for fam, pts in groups.items():
+        if len(pts) < 2:
+            continue
+        x = np.array([p[0] for p in pts])
+        t = np.array([p[1] for p in pts])
+        b, a = np.polyfit(x, t, 1)
+        fits.append({"family": fam, "sizes_bytes": [int(v) for v in x], "steady_GBps": round(1 / b / 1e9, 1),
+                     "steady_frac": round(1 / b / 1e9 / HBM_PEAK_GBS, 4), "fixed_us": round(a * 1e6, 2),
+                     "frac_per_size": [round(v / s / 1e9 / HBM_PEAK_GBS, 4) for v, s in zip(x, t)]})
+        log(f"[bench] sweep fit {fam}: steady {1 / b / 1e9:.0f} GB/s ({100 / b / 1e9 / HBM_PEAK_GBS:.1f}%), "
+            f"fixed {a * 1e6:.2f} us")
+    return fits
+
+
+def hbm_sweep(steps: int, flusher) -> tuple[list[dict], list[dict]]:
+    """C2 (4 reads + 1 write) and C3 (row reductions and broadcast tiled
+    streams) at 1x, 2x and 4x their BASELINE sizes, plus ``read_ceiling``
+    over C3's input, each launch after the cache flush.  Returns the
+    per-kernel records and the ``fit_sweep`` lines."""
+    from tests.gpu_cases import sigmoid_chain, softmax
+
+    recs = []
+    for s in SWEEP_SCALES:
+        for label, ops in ((f"sweep C2 x{s}", sigmoid_chain(4096 * s, 4096, seed=1)),
+                           (f"sweep C3 x{s}", softmax(8192 * s, 8192, seed=2))):
+            log(f"[bench] {label}: preparing")
+            prep = Prepared(ops)
+            recs += time_kernels(prep, steps, 2, flusher, label)
+            if label.startswith("sweep C3"):
+                recs += read_ceiling(prep.env["x"], 8192 * s * 8192 * 4, steps, flusher, f"sweep read x{s}")
+            prep.release()
+            del ops
+    return recs, fit_sweep(recs)
+
+
 def fragment_benches(steps: int, flusher) -> list[dict]:
     """The reference's fragment-level benches (tests/bench_init.py,
     bench_reduction.py, bench_elementwise.py, bench_matmul.py) at their own
@@ -871,6 +986,10 @@ def main() -> int:
         per_config += fragment_benches(max(3, min(args.steps, 10)), flush)
     if only == "ceilings":
         per_config += ceiling_benches(max(3, args.steps), flush)
+    sweep_fits = None
+    if only == "sweep":
+        recs, sweep_fits = hbm_sweep(max(3, args.steps), flush)
+        per_config += recs
 
     # ---- other configs -----------------------------------------------------
     if (not args.no_extra and only is None) or only not in (None, "fragments"):
@@ -908,6 +1027,8 @@ def main() -> int:
     if cpu_configs:
         line.setdefault("cpu_baseline", {})["per_config"] = cpu_configs
     line["per_kernel"] = per_config
+    if sweep_fits is not None:
+        line["hbm_sweep"] = sweep_fits
     if only is None and not args.no_extra:
         line["end_to_end"] = end_to_end_runs()
     print(json.dumps(line), flush=True)

@@ -1,0 +1,54 @@
+"""Host-side pieces of bench.py: the size-sweep fit and the read-ceiling
+kernel's launch contract (no GPU needed)."""
+
+import pytest
+
+import bench
+from metellus_amd.runtime import hip_backend
+
+
+def _records(rate_gbps, t0_us, sizes, config, kernel):
+    return [{"config": config.format(s=s), "kernel": kernel, "work": float(b),
+             "ms_mean": (t0_us * 1e-6 + b / (rate_gbps * 1e9)) * 1e3} for s, b in sizes]
+
+
+def test_fit_sweep_recovers_rate_and_fixed_cost():
+    sizes = [(1, 335544320), (2, 671088640), (4, 1342177280)]
+    recs = _records(6900.0, 2.7, sizes, "sweep C2 x{s}", "elementwise_out_fused")
+    recs += _records(7100.0, -1.9, [(s, 2 * b) for s, b in sizes], "sweep C3 x{s}", "elementwise_e_fused")
+    recs += _records(7000.0, 1.5, sizes, "sweep read x{s} grid 8192", "read_ceiling")
+    recs += _records(6800.0, 3.0, sizes, "sweep read x{s} grid 2048", "read_ceiling")
+    fits = {f["family"]: f for f in bench.fit_sweep(recs)}
+    assert set(fits) == {"sweep C2 / elementwise_out_fused", "sweep C3 / elementwise_e_fused",
+                         "sweep read / read_ceiling grid 8192", "sweep read / read_ceiling grid 2048"}
+    f = fits["sweep C2 / elementwise_out_fused"]
+    assert f["steady_GBps"] == pytest.approx(6900.0, abs=0.1) and f["fixed_us"] == pytest.approx(2.7, abs=0.01)
+    f = fits["sweep C3 / elementwise_e_fused"]
+    assert f["steady_GBps"] == pytest.approx(7100.0, abs=0.1) and f["fixed_us"] == pytest.approx(-1.9, abs=0.01)
+    assert fits["sweep read / read_ceiling grid 2048"]["steady_GBps"] == pytest.approx(6800.0, abs=0.1)
+    # per-size fractions: bytes / time / 8 TB/s
+    b, t = sizes[0][1], 2.7e-6 + sizes[0][1] / 6.9e12
+    assert fits["sweep C2 / elementwise_out_fused"]["frac_per_size"][0] == pytest.approx(b / t / 8e12, abs=1e-4)
+
+
+def test_read_ceiling_source_compiles_for_gfx950():
+    assert hip_backend.compile_only(bench.READ_CEILING_SRC) > 0
+
+
+class _FakeBuffer:
+    def __init__(self, nbytes):
+        self.nbytes = nbytes
+
+
+@pytest.mark.parametrize("nbytes", [8192 * 8192 * 4 + 4, (32768 * 5 + 2048) * 16, 8192 * 8192 * 8])
+def test_read_ceiling_rejects_sizes_its_grids_cannot_split(nbytes):
+    """Not a multiple of 16 bytes, a float4 count the grids do not divide, or
+    more bytes than the buffer holds: refused before anything launches."""
+    with pytest.raises(ValueError, match="read_ceiling"):
+        bench.read_ceiling(_FakeBuffer(8192 * 8192 * 4), nbytes, 1, None, "x")
+
+
+def test_read_ceiling_grids_divide_the_sweep_sizes():
+    for s in bench.SWEEP_SCALES:
+        n4 = 8192 * s * 8192 * 4 // 16
+        assert all(n4 % g == 0 and n4 // g >= 256 for g in bench.READ_CEILING_GRIDS)
