@@ -44,8 +44,22 @@ int mt_device_info(char* arch, size_t arch_len, int* cu_count, int* clock_khz);
 int mt_alloc(size_t nbytes, uint64_t* handle);
 
 /* release_buffer (reference: src/metal_backend.mm:101-103): *existed is 1 if
- * the handle was live, 0 if unknown/already released (not an error). */
+ * the handle was live, 0 if unknown/already released (not an error).  The
+ * device block is kept for reuse by later mt_alloc calls of its size class
+ * (blocks >= 2 MiB in 2 MiB steps, smaller ones in 256 B steps; a cached
+ * block serves a request up to 1/8 smaller) while the cache holds less than
+ * a quarter of the device (at most 64 GiB); returning device memory to the
+ * driver halves host<->device copy rates for the next ~50 ms on MI355X.
+ * Reuse is stream-ordered, as with hipFreeAsync. */
 int mt_free(uint64_t handle, int* existed);
+
+/* No counterpart in the reference (Metal buffers go back to the system when
+ * released).  Return every cached device block to the driver; mt_alloc also
+ * does this by itself when the device runs out of memory. */
+int mt_trim(void);
+
+/* Bytes and blocks in the device block cache (either pointer may be NULL). */
+int mt_cache_info(size_t* cached_bytes, size_t* cached_blocks);
 
 /* buffer_size (reference: src/metal_backend.mm:105-108). */
 int mt_size(uint64_t handle, size_t* nbytes);

@@ -62,6 +62,7 @@ struct DimsArg {
 struct Buffer {
     void* ptr;
     size_t nbytes;
+    size_t cap;  // bytes of the block behind ptr (>= nbytes; the device cache's size class)
 };
 
 struct Kernel {
@@ -92,6 +93,10 @@ struct State {
     std::unordered_map<void*, size_t> host_cap;
     std::multimap<size_t, void*> host_free;
     size_t host_cached = 0;
+    // Freed device blocks kept for reuse, by capacity (see mt_free).
+    std::multimap<size_t, void*> dev_free;
+    size_t dev_cached = 0;
+    size_t dev_cache_limit = 0;
     // Workspace of stream-K kernels (a registry buffer the shim owns).
     uint64_t ws_handle = 0;
     size_t ws_bytes = 0;
@@ -132,6 +137,25 @@ constexpr int kMaxLaunchBuffers = 64;
 
 constexpr size_t kHostGranule = size_t(64) << 10;     // pinned blocks are multiples of 64 KiB
 constexpr size_t kHostCacheLimit = size_t(1) << 30;   // at most 1 GiB of returned blocks kept
+
+// Device block cache.  Returning device memory to the driver makes every
+// host<->device copy of the next ~50 ms run at half speed on MI355X (a
+// 256 MiB download: 4.7 ms -> 8.7-10 ms after a free of 256-768 MiB,
+// measured with C3 run()s back to back; the copies themselves are unchanged).
+// hipFreeAsync returns the memory at once although the default pool's release
+// threshold is set to keep it (its reserved size drops to 0), so freed blocks
+// stay here instead and serve later allocations of their size class.  Reuse
+// is stream-ordered like hipFreeAsync: every copy, fill and launch of the shim
+// runs on its one stream, so work queued before a free finishes before the
+// block's next owner touches it.
+constexpr size_t kDevGranule = size_t(2) << 20;       // blocks >= 2 MiB: multiples of 2 MiB
+constexpr size_t kDevSmallGranule = 256;               // smaller blocks: multiples of 256 B
+constexpr size_t kDevCacheMax = size_t(64) << 30;      // at most 64 GiB (or a quarter of the device) kept
+
+size_t dev_capacity(size_t nbytes) {
+    const size_t g = nbytes >= kDevGranule ? kDevGranule : kDevSmallGranule;
+    return (nbytes + g - 1) / g * g;
+}
 
 State& state() {
     static State s;
@@ -306,6 +330,7 @@ int init_locked(State& s) {
     s.arch = prop.gcnArchName;
     s.cu_count = prop.multiProcessorCount;
     s.clock_khz = prop.clockRate;
+    s.dev_cache_limit = std::min(kDevCacheMax, static_cast<size_t>(prop.totalGlobalMem) / 4);
     MT_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
     // Timing-only events: without the system-scope release at record time
     // (an L2 write-back of the kernel's dirty lines), the bracket measures
@@ -490,17 +515,60 @@ int mt_device_info(char* arch, size_t arch_len, int* cu_count, int* clock_khz) {
     return 0;
 }
 
+// Hand every cached device block back to the driver (stream-ordered).
+static int release_dev_cache(State& s) {
+    for (auto& kv : s.dev_free) MT_HIP(hipFreeAsync(kv.second, s.stream));
+    s.dev_free.clear();
+    s.dev_cached = 0;
+    return 0;
+}
+
 int mt_alloc(size_t nbytes, uint64_t* handle) {
     if (!handle) return fail("mt_alloc: null output");
     if (nbytes == 0) return fail("create_buffer: nbytes must be > 0");
     State& s = state();
     std::lock_guard<std::mutex> lock(s.mu);
     if (init_locked(s)) return 1;
+    const size_t cap = dev_capacity(nbytes);
     void* p = nullptr;
-    MT_HIP(hipMallocAsync(&p, nbytes, s.stream));
+    size_t got = cap;
+    // The smallest cached block of at least cap bytes, wasting at most 1/8.
+    auto it = s.dev_free.lower_bound(cap);
+    if (it != s.dev_free.end() && it->first <= cap + cap / 8) {
+        p = it->second;
+        got = it->first;
+        s.dev_cached -= got;
+        s.dev_free.erase(it);
+    } else {
+        hipError_t e = hipMallocAsync(&p, cap, s.stream);
+        if (e == hipErrorOutOfMemory && !s.dev_free.empty()) {
+            (void)hipGetLastError();
+            if (release_dev_cache(s)) return 1;
+            MT_HIP(hipStreamSynchronize(s.stream));
+            e = hipMallocAsync(&p, cap, s.stream);
+        }
+        if (e != hipSuccess) return fail(std::string("hipMallocAsync: ") + hipGetErrorString(e));
+    }
     uint64_t h = s.next_buffer++;
-    s.buffers.emplace(h, Buffer{p, nbytes});
+    s.buffers.emplace(h, Buffer{p, nbytes, got});
     *handle = h;
+    return 0;
+}
+
+int mt_trim(void) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (!s.ready) return 0;
+    if (release_dev_cache(s)) return 1;
+    MT_HIP(hipStreamSynchronize(s.stream));
+    return 0;
+}
+
+int mt_cache_info(size_t* cached_bytes, size_t* cached_blocks) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (cached_bytes) *cached_bytes = s.dev_cached;
+    if (cached_blocks) *cached_blocks = s.dev_free.size();
     return 0;
 }
 
@@ -513,11 +581,18 @@ int mt_free(uint64_t handle, int* existed) {
         if (existed) *existed = 0;
         return 0;
     }
-    void* p = it->second.ptr;
+    const Buffer b = it->second;
     s.buffers.erase(it);
     if (existed) *existed = 1;
-    // Stream-ordered: kernels already queued that read the buffer finish first.
-    MT_HIP(hipFreeAsync(p, s.stream));
+    // Kept for reuse (the device block cache) while the cache has room;
+    // otherwise returned, stream-ordered: kernels already queued that read
+    // the buffer finish first either way.
+    if (s.dev_cached + b.cap <= s.dev_cache_limit) {
+        s.dev_free.emplace(b.cap, b.ptr);
+        s.dev_cached += b.cap;
+        return 0;
+    }
+    MT_HIP(hipFreeAsync(b.ptr, s.stream));
     return 0;
 }
 
@@ -799,7 +874,7 @@ int mt_workspace(size_t nbytes, uint64_t* handle) {
         MT_HIP(hipMallocAsync(&p, nbytes, s.stream));
         MT_HIP(hipMemsetAsync(p, 0, kWsHeadBytes, s.stream));  // flags and error word start at 0
         s.ws_handle = s.next_buffer++;
-        s.buffers.emplace(s.ws_handle, Buffer{p, nbytes});
+        s.buffers.emplace(s.ws_handle, Buffer{p, nbytes, nbytes});
         s.ws_bytes = nbytes;
     }
     *handle = s.ws_handle;

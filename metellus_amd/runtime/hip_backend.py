@@ -34,6 +34,8 @@ EXPORTED_SYMBOLS = (
     "mt_device_info",
     "mt_alloc",
     "mt_free",
+    "mt_trim",
+    "mt_cache_info",
     "mt_size",
     "mt_device_ptr",
     "mt_write",
@@ -87,6 +89,8 @@ def _load():
             ),
             "mt_alloc": ([ctypes.c_size_t, ctypes.POINTER(_u64)], ctypes.c_int),
             "mt_free": ([_u64, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+            "mt_trim": ([], ctypes.c_int),
+            "mt_cache_info": ([ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
             "mt_size": ([_u64, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
             "mt_device_ptr": ([_u64, ctypes.POINTER(_u64)], ctypes.c_int),
             "mt_write": ([_u64, ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int),
@@ -191,6 +195,19 @@ def release_buffer(handle: int) -> bool:
     existed = ctypes.c_int(0)
     _check(_load().mt_free(int(handle), ctypes.byref(existed)))
     return bool(existed.value)
+
+
+def trim() -> None:
+    """Return the shim's cached device blocks (freed buffers kept for reuse)
+    to the driver."""
+    _check(_load().mt_trim())
+
+
+def device_cache_info() -> tuple[int, int]:
+    """(bytes, blocks) held in the shim's device block cache."""
+    nb, nk = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    _check(_load().mt_cache_info(ctypes.byref(nb), ctypes.byref(nk)))
+    return nb.value, nk.value
 
 
 def buffer_size(handle: int) -> int:
