@@ -161,9 +161,11 @@ def test_shape_kernel_strides_and_launch():
     g = assemble(fuse(ops.build())[0])
     src = g.kernel.source
     # a transposed view (row stride 1, column stride 8): LDS-tiled transpose
-    # reading the owner's buffer along its contiguous axis, 128-bit wide
-    assert "mt_ld4(g_X + (size_t)(j0 + jj) * 8u + i0 + l4)" in src
-    assert "__shared__ alignas(16) float copy_tile[64][65];" in src
+    # reading the owner's buffer along its contiguous axis, 128-bit wide,
+    # streaming loads and device-scope stores; 128 x 64 tiles, odd LDS pitch
+    assert "mt_ld4_nt(g_X + (size_t)(j0 + jj) * 8u + i0 + li)" in src
+    assert "mt_st4_wt(g_Y + (size_t)(i0 + ii) * 4u + j0 + sj" in src
+    assert "__shared__ alignas(16) float copy_tile[64][129];" in src
     assert g.bindings == ("X", "Y") and g.dims == (32,)
     assert hip_backend.compile_only(src) > 0
     ops = Operations()  # 13 x 10 transposed view: scalar tiles
