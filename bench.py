@@ -812,6 +812,9 @@ def read_profile_traffic(config: str, kernel: str, name: str = "bench_kernels_pm
 
 
 C4_LABEL = "C4 MLP literal"
+# The same C4 program with the multi-anchor merge-chain extension
+# (orchestrator.fusion.MULTI_ANCHOR_MERGE_CHAINS): the gate in one kernel.
+C4_EXT_LABEL = "C4 MLP literal, gate fused (extension)"
 C4_FLOPS = 3 * 2 * 4096 * 4096 * 11008  # 1.108 TFLOP of matmul work per step
 
 
@@ -1004,6 +1007,7 @@ def main() -> int:
         if only in (None, "c4"):
             todo.append(("C4 MLP literal", lambda: _c4(False)))
             todo.append(("C4 MLP diamond", lambda: _c4(True)))
+            todo.append((C4_EXT_LABEL, lambda: _c4(False)))
         if only in (None, "c5"):
             todo.append(("C5 attention, 32 heads batched", lambda: [_c5(h) for h in range(32)]))
         if only in (None, "copy"):
@@ -1011,11 +1015,19 @@ def main() -> int:
         for label, make in todo:
             log(f"[bench] {label}: preparing")
             made = make()
-            prep = PreparedBatch(made) if isinstance(made, list) else Prepared(made)
+            from metellus_amd.orchestrator import fusion
+
+            saved, fusion.MULTI_ANCHOR_MERGE_CHAINS = fusion.MULTI_ANCHOR_MERGE_CHAINS, label == C4_EXT_LABEL
+            try:
+                prep = PreparedBatch(made) if isinstance(made, list) else Prepared(made)
+            finally:
+                fusion.MULTI_ANCHOR_MERGE_CHAINS = saved
             per_config += time_kernels(prep, extra_steps, 2, flush, label)
             if label.startswith("C2"):
                 check_c2(prep)
             prep.release()
+            if label == C4_EXT_LABEL:  # the same program as C4 literal: its CPU time is that line's
+                continue
             if not args.no_cpu and not (label == C4_LABEL and line is not None):  # the headline timed C4 already
                 cpu = cpu_baseline_config(label, made, per_config)
                 if cpu is not None:

@@ -25,6 +25,9 @@ class DecisionView:
     ops: tuple[Op, ...] = ()
     anchors: tuple[MatmulOp, ...] = ()
     merge_elem: ElementwiseOp | None = None
+    # the merge ops in program order (the reference's one op, or a chain from
+    # the MULTI_ANCHOR_MERGE_CHAINS extension); merge_elem is the last
+    merge_chain: tuple[ElementwiseOp, ...] = ()
     shared_a: bool = False
     prologues_a: tuple[tuple[ElementwiseOp, ...], ...] = ()
     prologues_b: tuple[tuple[ElementwiseOp, ...], ...] = ()
@@ -63,15 +66,22 @@ def _classify_multi_anchor(ops: tuple[Op, ...], anchors: tuple[MatmulOp, ...]) -
     a0, a1 = anchors
     i0, i1 = ops.index(a0), ops.index(a1)
     tail = ops[max(i0, i1) + 1 :]
-    assert len(tail) == 1 and isinstance(tail[0], ElementwiseOp), "v0: multi-anchor vertex has exactly one merge elem"
-    merge = tail[0]
+    if len(tail) > 1:
+        from metellus_amd.orchestrator import fusion
+
+        assert fusion.MULTI_ANCHOR_MERGE_CHAINS and all(isinstance(op, ElementwiseOp) for op in tail), (
+            "v0: multi-anchor vertex has exactly one merge elem"
+        )
+    assert tail and isinstance(tail[0], ElementwiseOp), "v0: multi-anchor vertex has exactly one merge elem"
+    merge = tail[-1]
     pre0 = tuple(op for op in ops[:i0] if isinstance(op, ElementwiseOp))
     pre1 = tuple(op for op in ops[:i1] if isinstance(op, ElementwiseOp))
     pro_a = (trace_prologue(a0.a.name, pre0), trace_prologue(a1.a.name, pre1))
     pro_b = (trace_prologue(a0.b.name, pre0), trace_prologue(a1.b.name, pre1))
     covered = {id(op) for chain in (*pro_a, *pro_b) for op in chain}
+    covered |= {id(op) for op in tail}
     for op in ops:
-        if isinstance(op, ElementwiseOp) and op is not merge:
+        if isinstance(op, ElementwiseOp):
             assert id(op) in covered, (
                 f"v0: pre-anchor elementwise op {op.out.name!r} not absorbed by any anchor prologue"
             )
@@ -81,6 +91,7 @@ def _classify_multi_anchor(ops: tuple[Op, ...], anchors: tuple[MatmulOp, ...]) -
         strategy=FusionStrategy.DIAMOND_SHARED if shared else FusionStrategy.MULTI_PRODUCER_CONVERGENT,
         anchors=anchors,
         merge_elem=merge,
+        merge_chain=tuple(tail),
         shared_a=shared,
         prologues_a=pro_a,
         prologues_b=pro_b,

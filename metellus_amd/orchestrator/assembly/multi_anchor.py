@@ -91,7 +91,10 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
 
     tf_a = tuple(prologue(pro_a[i], src_a[i], f"prologue_a{i}") for i in range(2))
     tf_b = tuple(prologue(pro_b[i], src_b[i], f"prologue_b{i}") for i in range(2))
-    merge_code = ChainCode((merge,), (a0.out.name, a1.out.name), "merge")  # IEEE division: the output
+    merge_chain = decision.merge_chain or (merge,)
+    merge_code = ChainCode(merge_chain, (a0.out.name, a1.out.name), "merge")  # IEEE division: the output
+    if merge_code.externals:
+        raise ValueError("multi-anchor: the merge reads tensors other than the two matmul outputs")
     helpers.append(merge_code.helper())
     value_expr = merge_code.call(["{a0}", "{a1}"], [])
 
@@ -189,7 +192,10 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
     else:
         dim_names, dim_values = ("M", "K0", "K1", "N"), (M, K0, K1, N)
     ctx = CodegenContext(
-        function_name=function_name or f"multi_anchor_{merge.out.name}_fused",
+        # the reference's name; a merge chain (an extension) is named apart
+        function_name=function_name or (
+            f"multi_anchor_{merge.out.name}_fused" if len(merge_chain) == 1 else f"multi_anchor_chain_{merge.out.name}_fused"
+        ),
         buffers=(*(input_param(k) for k in keys), output_param(out_key), *extras.buffers),
         dims=dim_names,
         tg_x=tile.tg_x,

@@ -13,6 +13,11 @@ the top, until nothing fires ("saturation"):
 4. ``try_prologue_absorb_single`` elem -> anchor input (unique consumer)
 5. ``try_prologue_absorb_multi``  lane-agnostic elem recomputed in 2+ anchors
 
+An extension beyond the reference, off by default
+(``MULTI_ANCHOR_MERGE_CHAINS``), runs between 1 and 2:
+``try_multi_producer_chain_fuse`` merges two matmuls through a chain of
+elementwise ops instead of one (the MLP gate ``silu(X @ W1) * (X @ W2)``).
+
 Budget gate: each rewrite's new vertices are assembled and their LDS plan
 measured; a rewrite that exceeds the cap is blacklisted by its op-id
 signature and fusion restarts from the primitive graph.
@@ -248,6 +253,66 @@ def try_multi_producer_fuse(graph: Graph, blacklist: Blacklist) -> Graph | None:
     return None
 
 
+# Extension beyond the reference's rules, off by default: the two matmuls
+# of a multi-anchor kernel may merge through a chain of elementwise ops --
+# each op reading the two matmul outputs, scalars and earlier ops of the
+# chain, e.g. silu(X @ W1) * (X @ W2) = (h1 * recip(1 + exp(-h1))) * h2 --
+# instead of one binary op.  The reference fuses only the one-op merge
+# (fusion.py:219-247 here, its try_multi_producer_fuse); with this flag the
+# MLP block's gate becomes one DIAMOND_SHARED kernel writing the gated
+# product, and the matmul after it loads that product directly.
+MULTI_ANCHOR_MERGE_CHAINS = False
+
+
+def try_multi_producer_chain_fuse(graph: Graph, blacklist: Blacklist) -> Graph | None:
+    """(Extension, ``MULTI_ANCHOR_MERGE_CHAINS``.)  Two single-matmul vertices
+    of equal output shape and the elementwise vertices that read them: the
+    merge set grows from the matmuls' readers through the readers of its own
+    values, stopping at the first reader that is not elementwise.  It fuses
+    when every tensor it reads is one of the two matmul outputs or its own
+    (no other tensors), it comes after both matmuls in program order, and
+    exactly one of its values -- its last op's -- is read outside it or is a
+    program output.  The one-op merge is left to the reference's pass."""
+    if not MULTI_ANCHOR_MERGE_CHAINS:
+        return None
+    mats = [v for v in graph.vertices if len(v.ops) == 1 and isinstance(v.ops[0], MatmulOp)]
+    for i, pa in enumerate(mats):
+        for pb in mats[i + 1:]:
+            ma, mb = pa.ops[0], pb.ops[0]
+            if ma.out.shape != mb.out.shape:
+                continue
+            seeds = (ma.out.name, mb.out.name)
+            members: list[Vertex] = []
+            queue = [c for name in seeds for c in graph.consumers_of(name)]
+            while queue:
+                v = queue.pop()
+                if any(v is m for m in members) or v is pa or v is pb or not _is_elementwise_vertex(v):
+                    continue
+                members.append(v)
+                queue.extend(c for name in v.outputs for c in graph.consumers_of(name))
+            if not members or (len(members) == 1 and len(members[0].ops) == 1):
+                continue
+            chain = _by_position(graph, tuple(op for v in members for op in v.ops))
+            made = set(seeds) | {op.out.name for op in chain}
+            if any(isinstance(o, Tensor) and o.name not in made for op in chain for o in op.operands):
+                continue
+            last_anchor = max(graph.op_index[id(ma)], graph.op_index[id(mb)])
+            if graph.op_index[id(chain[0])] < last_anchor:
+                continue
+            inside = {id(v) for v in (pa, pb, *members)}
+            escaping = {
+                name for name in made
+                if name in graph.program_outputs or any(id(c) not in inside for c in graph.consumers_of(name))
+            }
+            if escaping != {chain[-1].out.name}:
+                continue
+            ops = _by_position(graph, (ma, mb, *chain))
+            if frozenset(id(op) for op in ops) in blacklist:
+                continue
+            return graph.replace(absorbed=(pa, pb, *members), ops=ops)
+    return None
+
+
 def _should_recompute(elem: ElementwiseOp) -> bool:
     """Recompute a shared prologue only when it is lane-agnostic: each
     consumer can rebuild it from the primary it already loads."""
@@ -293,6 +358,7 @@ def try_prologue_absorb_multi(graph: Graph, blacklist: Blacklist) -> Graph | Non
 
 _PASSES = (
     try_elem_chain_fuse,
+    try_multi_producer_chain_fuse,  # extension, off unless MULTI_ANCHOR_MERGE_CHAINS
     try_multi_producer_fuse,  # must precede epilogue absorption (it would steal the merge)
     try_epilogue_absorb,
     try_prologue_absorb_single,
