@@ -612,13 +612,24 @@ MT_INLINE unsigned mt_lds_addr(const float* p) {
     return (unsigned)(unsigned long long)(const __attribute__((address_space(3))) float*)p;
 }
 
-// 16 bytes from g to LDS byte address lds_byte + 16 * lane (lds_byte wave
-// uniform).  One wait state separates the M0 write from the load reading it.
-MT_INLINE void mt_dma16(const float* g, unsigned lds_byte) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+// 16 bytes from sbase + voff to LDS byte address lds_byte + 16 * lane:
+// sbase is a wave-uniform address held in scalar registers, voff this lane's
+// 32-bit byte offset from it, lds_byte wave uniform.  One wait state
+// separates the M0 write from the load reading it.
+MT_INLINE void mt_dma16(unsigned long long sbase, unsigned voff, unsigned lds_byte) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                  :
-                 : "v"(g), "s"(lds_byte)
+                 : "v"(voff), "s"(sbase), "s"(lds_byte)
                  : "memory", "m0");
+}
+
+// A wave-uniform address as a scalar value (both halves read from the first
+// lane; the compiler folds this when the address is already scalar).
+MT_INLINE unsigned long long mt_uniform_addr(const float* p) {
+    const unsigned long long a = (unsigned long long)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+    return ((unsigned long long)hi << 32) | lo;
 }
 
 // Where a direct-to-LDS load puts its data: lane `lane` of wave-load `inst`
@@ -637,6 +648,15 @@ MT_HD void mt_dma_slot(unsigned inst, unsigned lane, unsigned& r, unsigned& logi
 // 4; 16-byte aligned base) at (row0, col0), every element in bounds, into a
 // dense LDS tile; SWZ permutes each row's slots by mt_swz.  Wave w issues
 // wave-loads w PERW .. w PERW + PERW - 1, each 1 KiB of contiguous LDS.
+//
+// The loader is built once per kernel with the source's row stride: each
+// lane's byte offsets from the tile origin do not change from chunk to
+// chunk, so they are computed there, and a fetch adds only the tile
+// origin -- a scalar address -- through the load's scalar-base form.  The
+// offsets are 32-bit: ((ROWS - 1) rs + COLS) * 4 must stay below 2^32 (the
+// assembler checks).  Recomputing the full per-lane addresses in every
+// chunk cost ~900 cycles of VALU work per 32-wide chunk on a 256x256 tile
+// (4096^3 GEMM, measured in shader cycles per workgroup: 2.26 -> 2.19 M).
 template <int ROWS, int COLS, int NT, bool SWZ>
 struct mt_tile_dma {
     static constexpr int S = COLS / 4;
@@ -644,19 +664,30 @@ struct mt_tile_dma {
     static constexpr int PERW = INSTR / (NT / 64);
     static_assert(COLS % 4 == 0 && (ROWS * S) % 64 == 0 && INSTR % (NT / 64) == 0,
                   "the tile must split into whole 1 KiB wave loads, the same number per wave");
+    unsigned off[PERW];  // this lane's byte offset of each of the wave's loads
+    unsigned lds_off;    // byte offset of the wave's first load in the tile (uniform)
 
-    MT_INLINE void fetch(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0,
-                         float* lds, unsigned tid, int part = 0, int parts = 1) const {
+    MT_INLINE mt_tile_dma(unsigned rs, unsigned tid) {
         const unsigned lane = tid & 63u;
         const unsigned wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-        const unsigned base = __builtin_amdgcn_readfirstlane(mt_lds_addr(lds));
+        lds_off = wave * PERW * 1024u;
+#pragma unroll
+        for (int q = 0; q < PERW; ++q) {
+            unsigned r, logical;
+            mt_dma_slot<S, SWZ>(wave * PERW + q, lane, r, logical);
+            off[q] = (r * rs + 4u * logical) * 4u;
+        }
+    }
+
+    // rs: the row stride the loader was built with.
+    MT_INLINE void fetch(const float* __restrict__ src, unsigned rs, unsigned row0, unsigned col0, float* lds,
+                         int part = 0, int parts = 1) const {
+        const unsigned long long origin = mt_uniform_addr(src + (size_t)row0 * rs + col0);
+        const unsigned base = __builtin_amdgcn_readfirstlane(mt_lds_addr(lds)) + lds_off;
 #pragma unroll
         for (int q = 0; q < PERW; ++q) {
             if (!mt_in_part(q, PERW, part, parts)) continue;
-            const unsigned inst = wave * PERW + q;
-            unsigned r, logical;
-            mt_dma_slot<S, SWZ>(inst, lane, r, logical);
-            mt_dma16(src + (size_t)(row0 + r) * rs + col0 + 4u * logical, base + inst * 1024u);
+            mt_dma16(origin, off[q], base + (unsigned)q * 1024u);
         }
     }
 };

@@ -61,6 +61,15 @@ def _is_int(s: str) -> bool:
     return True
 
 
+def dma_offsets_fit(rows: int, cols: int, row_stride) -> bool:
+    """A direct-to-LDS loader keeps each lane's byte offset from the tile
+    origin in 32 bits (``mt_tile_dma``): the row stride must be a literal and
+    the farthest element of a rows x cols tile within 2^32 bytes."""
+    if not _is_int(str(row_stride)):
+        return False
+    return ((rows - 1) * int(row_stride) + cols) * 4 < 1 << 32
+
+
 @dataclass(frozen=True)
 class TgLoadFragment:
     name: str
@@ -167,6 +176,9 @@ class TgLoadFragment:
         slots = rows * cols // 4
         if cols % 4 or slots % 64 or (slots // 64) % (self.num_threads // 64):
             raise ValueError(f"{self.name}: a {rows}x{cols} tile does not split into whole wave loads")
+        if not dma_offsets_fit(rows, cols, self.src_row_stride):
+            raise ValueError(f"{self.name}: a {rows}x{cols} tile at row stride {self.src_row_stride} needs "
+                             "per-lane offsets beyond 32 bits")
 
     def render_decl(self) -> str:
         rows, cols = self.tile_shape
@@ -174,7 +186,8 @@ class TgLoadFragment:
         if mode == "dma":
             self._check_dma()
             swz = "true" if self.dma_swizzle else "false"
-            return f"const mt_tile_dma<{rows}, {cols}, {self.num_threads}, {swz}> {self.loader};"
+            return (f"const mt_tile_dma<{rows}, {cols}, {self.num_threads}, {swz}> "
+                    f"{self.loader}({self.src_row_stride}, threadIdx.x);")
         tmpl = {"colvec": "mt_tile_colvec", "colvec_safe": "mt_tile_colvec", "rowvec": "mt_tile_rowvec",
                 "scalar": "mt_tile_scalar"}[mode]
         if self.gathering:
@@ -222,7 +235,7 @@ class TgLoadFragment:
                 raise ValueError(f"{self.name}: a direct-to-LDS fetch needs its LDS stage")
             return (
                 f"{self.loader}.fetch({self.src_name}, {self.src_row_stride}, {self.row_start}, "
-                f"{self.col_start}, {self.stage_ptr(stage)}, {tid});"
+                f"{self.col_start}, {self.stage_ptr(stage)});"
             )
         rlim = self.row_limit if self.row_limit is not None else "0xffffffffu"
         clim = self.col_limit if self.col_limit is not None else "0xffffffffu"

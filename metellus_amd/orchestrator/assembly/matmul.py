@@ -44,7 +44,7 @@ from metellus_amd.compute.matmul.matmul import (
     ThreadIndexFragment,
     stream_k_workspace_bytes,
 )
-from metellus_amd.memory.memory import TgLoadFragment
+from metellus_amd.memory.memory import TgLoadFragment, dma_offsets_fit
 from metellus_amd.orchestrator.assembly.decision import DecisionView
 from metellus_amd.orchestrator.assembly.expressions import ChainCode
 from metellus_amd.orchestrator.assembly.extras import Extras, input_param, output_param, param_name
@@ -173,20 +173,25 @@ def dma_layouts(tile: TileConfig, srcs_a, srcs_b, pros_a, pros_b, aligned: bool)
     if not DMA_LOADS or not aligned or tile.stages != 2:
         return tile
     nt = tile.num_threads
-    swz_k = tile.tile_K in (16, 32)
+    tm, tn, tk = tile.tile_M, tile.tile_N, tile.tile_K
+    swz_k = tk in (16, 32)
     a_ok = (
         swz_k
         and all(p is None and t.col_stride == 1 and t.row_stride % 4 == 0 for t, p in zip(srcs_a, pros_a))
-        and _dma_fits(tile.tile_M, tile.tile_K, nt)
+        and all(dma_offsets_fit(tm, tk, t.row_stride) for t in srcs_a)
+        and _dma_fits(tm, tk, nt)
     )
     b_layout = "pad"
     if all(p is None for p in pros_b):
-        if all(t.col_stride == 1 and t.row_stride % 4 == 0 for t in srcs_b) and _dma_fits(tile.tile_K, tile.tile_N, nt):
+        if (
+            all(t.col_stride == 1 and t.row_stride % 4 == 0 and dma_offsets_fit(tk, tn, t.row_stride) for t in srcs_b)
+            and _dma_fits(tk, tn, nt)
+        ):
             b_layout = "dense"
         elif (
             swz_k
-            and all(t.row_stride == 1 and t.col_stride % 4 == 0 for t in srcs_b)
-            and _dma_fits(tile.tile_N, tile.tile_K, nt)
+            and all(t.row_stride == 1 and t.col_stride % 4 == 0 and dma_offsets_fit(tn, tk, t.col_stride) for t in srcs_b)
+            and _dma_fits(tn, tk, nt)
         ):
             b_layout = "nswz"
     return dataclasses.replace(tile, a_layout="swz" if a_ok else "pad", b_layout=b_layout)

@@ -161,3 +161,27 @@ def test_assembler_picks_dma_layouts():
     # ragged shapes keep the bounds-checked register path
     g = by(gpu_cases.plain_matmul(100, 70, 130))["matmul_C_fused"]
     assert "mt_tile_dma<" not in g.kernel.source
+
+
+def test_dma_offsets_stay_within_32_bits():
+    """A direct-to-LDS loader keeps each lane's byte offset from the tile
+    origin in 32 bits; a row stride that would overflow them keeps that
+    operand on the register path."""
+    from metellus_amd.compute.matmul.config import TileConfig
+    from metellus_amd.memory.memory import dma_offsets_fit
+    from metellus_amd.orchestrator.assembly.matmul import dma_layouts
+    from metellus_amd.orchestrator.ir import Tensor
+
+    assert dma_offsets_fit(256, 32, 4096) and dma_offsets_fit(256, 32, "4096")
+    # farthest byte: ((rows - 1) * rs + cols) * 4 against 2^32
+    edge = ((1 << 30) - 32) // 255
+    assert dma_offsets_fit(256, 32, edge) and not dma_offsets_fit(256, 32, edge + 1)
+    assert not dma_offsets_fit(32, 256, "K")  # a stride that is not a literal
+    tile = TileConfig(256, 256, 32, 2, 8)
+    near = Tensor("A", (256, 32), row_stride=4096)
+    far = Tensor("A", (256, 32), row_stride=(edge + 4) // 4 * 4)
+    b = Tensor("B", (32, 256))
+    assert dma_layouts(tile, (near,), (b,), (None,), (None,), True).a_layout == "swz"
+    assert dma_layouts(tile, (far,), (b,), (None,), (None,), True).a_layout == "pad"
+    b_far = Tensor("B", (32, 256), row_stride=(1 << 32) // 31 // 4 * 4)
+    assert dma_layouts(tile, (near,), (b_far,), (None,), (None,), True).b_layout == "pad"
