@@ -212,7 +212,7 @@ class PreparedBatch:
         k = g.kernel.batched()
         return self.hip.launch(
             k.handle, self.tables[i], g.dims, k.dims_slot_index,
-            (g.grid[0], g.grid[1], g.grid[2] * self.B), g.threads, timed=timed,
+            (g.grid[0], g.grid[1], g.grid[2] * self.B), g.threads, timed=timed, workspace=k.workspace_bytes,
         )
 
     def release(self):
@@ -815,6 +815,10 @@ C4_LABEL = "C4 MLP literal"
 # The same C4 program with the multi-anchor merge-chain extension
 # (orchestrator.fusion.MULTI_ANCHOR_MERGE_CHAINS): the gate in one kernel.
 C4_EXT_LABEL = "C4 MLP literal, gate fused (extension)"
+# C5 with the matmul -> reduction epilogue extension
+# (orchestrator.fusion.MATMUL_REDUCTION_EPILOGUES): m1 = max(S) in S's kernel.
+C5_EXT_LABEL = "C5 attention, row max fused (extension)"
+EXTENSION_FLAGS = {C4_EXT_LABEL: "MULTI_ANCHOR_MERGE_CHAINS", C5_EXT_LABEL: "MATMUL_REDUCTION_EPILOGUES"}
 C4_FLOPS = 3 * 2 * 4096 * 4096 * 11008  # 1.108 TFLOP of matmul work per step
 
 
@@ -1010,6 +1014,7 @@ def main() -> int:
             todo.append((C4_EXT_LABEL, lambda: _c4(False)))
         if only in (None, "c5"):
             todo.append(("C5 attention, 32 heads batched", lambda: [_c5(h) for h in range(32)]))
+            todo.append((C5_EXT_LABEL, lambda: [_c5(h) for h in range(32)]))
         if only in (None, "copy"):
             todo.append(("shape copy: transposed 4096x4096 view", _copy))
         for label, make in todo:
@@ -1017,16 +1022,19 @@ def main() -> int:
             made = make()
             from metellus_amd.orchestrator import fusion
 
-            saved, fusion.MULTI_ANCHOR_MERGE_CHAINS = fusion.MULTI_ANCHOR_MERGE_CHAINS, label == C4_EXT_LABEL
+            saved = {f: getattr(fusion, f) for f in EXTENSION_FLAGS.values()}
+            for f in saved:
+                setattr(fusion, f, EXTENSION_FLAGS.get(label) == f)
             try:
                 prep = PreparedBatch(made) if isinstance(made, list) else Prepared(made)
             finally:
-                fusion.MULTI_ANCHOR_MERGE_CHAINS = saved
+                for f, v in saved.items():
+                    setattr(fusion, f, v)
             per_config += time_kernels(prep, extra_steps, 2, flush, label)
             if label.startswith("C2"):
                 check_c2(prep)
             prep.release()
-            if label == C4_EXT_LABEL:  # the same program as C4 literal: its CPU time is that line's
+            if label in EXTENSION_FLAGS:  # the same program as its reference line: its CPU time is that line's
                 continue
             if not args.no_cpu and not (label == C4_LABEL and line is not None):  # the headline timed C4 already
                 cpu = cpu_baseline_config(label, made, per_config)

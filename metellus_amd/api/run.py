@@ -106,6 +106,7 @@ class BatchRunner:
                 (head.grid[0], head.grid[1], head.grid[2] * B),
                 head.threads,
                 timed=head.time_key is not None,
+                workspace=kernel.workspace_bytes,
             )
             if head.time_key is not None:
                 for env in envs:

@@ -68,6 +68,9 @@ class CodegenContext:
     # Bytes of device workspace the kernel takes as its last parameter
     # (``float* mt_ws``, after the dims); 0 = none.
     workspace_bytes: int = 0
+    # The kernel indexes its workspace by blockIdx.z, so its batched variant
+    # shares one workspace (workspace_bytes covers the batch it was built for).
+    workspace_batched: bool = False
 
     @property
     def num_threads(self) -> int:
@@ -179,7 +182,7 @@ class CodegenEngine:
             params, picks = list(ctx.buffers), []
         params.insert(dims_index, "const mt_dims dims")
         if ctx.workspace_bytes:
-            if ctx.batched:
+            if ctx.batched and not ctx.workspace_batched:
                 raise ValueError(f"{ctx.function_name}: a kernel with a workspace is not batched")
             params.append("float* mt_ws")
         body_parts = [

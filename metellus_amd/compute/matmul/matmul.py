@@ -69,6 +69,11 @@ class PersistentTiles:
     stream_k: bool = False
     tile_K: int = 32
     K_dim_var: str = "K"
+    # Row-block order instead: workgroup x takes row blocks x, x + P, ...
+    # and walks all column tiles of each in order (``mt_rr_first`` /
+    # ``mt_rr_last`` mark a row block's first and last tile), so a row
+    # reduction in the epilogue completes inside the workgroup.
+    row_blocks: bool = False
 
 
 def stream_k_workspace_bytes(tile_M: int, tile_N: int, workgroups: int, anchors: int = 1) -> int:
@@ -123,6 +128,28 @@ class MatmulTileMappingFragment:
                     "if (mt_has_next) mt_sk.item(mt_item + 1u, mt_t_next, mt_next_kb, mt_next_ke);",
                     f"const unsigned mt_next_m0 = (mt_t_next / mt_tiles_x) * {p.tile_M}u;",
                     f"const unsigned mt_next_n0 = (mt_t_next % mt_tiles_x) * {p.tile_N}u;",
+                    "const uint3 tg = make_uint3(mt_t % mt_tiles_x, mt_t / mt_tiles_x, blockIdx.z);",
+                ]
+            )
+        if p.row_blocks:
+            return "\n".join(
+                [
+                    *head,
+                    f"const unsigned mt_tiles_y = ({p.M_dim_var} + {p.tile_M - 1}u) / {p.tile_M}u;",
+                    "const unsigned mt_items = mt_tiles_y > blockIdx.x"
+                    " ? (mt_tiles_y - blockIdx.x + gridDim.x - 1u) / gridDim.x * mt_tiles_x : 0u;",
+                    "for (unsigned mt_i = 0u; mt_i < mt_items; ++mt_i) {",
+                    "const unsigned mt_t = (blockIdx.x + (mt_i / mt_tiles_x) * gridDim.x) * mt_tiles_x + mt_i % mt_tiles_x;",
+                    "const bool mt_first_tile = mt_i == 0u;",
+                    "const bool mt_rr_first = mt_i % mt_tiles_x == 0u;",
+                    "const bool mt_rr_last = mt_i % mt_tiles_x == mt_tiles_x - 1u;",
+                    "const bool mt_has_next = mt_i + 1u < mt_items;",
+                    "const unsigned mt_t_next = (blockIdx.x + ((mt_i + 1u) / mt_tiles_x) * gridDim.x) * mt_tiles_x"
+                    " + (mt_i + 1u) % mt_tiles_x;",
+                    f"const unsigned mt_next_m0 = (mt_t_next / mt_tiles_x) * {p.tile_M}u;",
+                    f"const unsigned mt_next_n0 = (mt_t_next % mt_tiles_x) * {p.tile_N}u;",
+                    "const unsigned mt_kb = 0u, mt_next_kb = 0u;",
+                    f"const unsigned mt_ke = ({p.K_dim_var} + {p.tile_K - 1}u) / {p.tile_K}u;",
                     "const uint3 tg = make_uint3(mt_t % mt_tiles_x, mt_t / mt_tiles_x, blockIdx.z);",
                 ]
             )
@@ -570,6 +597,188 @@ class MatmulEpilogueStoreFragment:
         return ()
 
 
+_RR_OPS = {"sum": (0, "0.0f"), "max": (1, "(-INFINITY)"), "min": (2, "INFINITY"), "product": (3, "1.0f")}
+
+
+@dataclass(frozen=True)
+class MatmulRowReduceStoreFragment:
+    """(Extension: the matmul -> reduction epilogue.)  Store the tile like
+    ``MatmulEpilogueStoreFragment``, then reduce each of its rows with
+    ``op`` into ``red_name[row]`` across the tiles of the row:
+
+    * the workgroup's previous tile, if any, is published first
+      (``mt_rr_finish``): its writes completed during this tile's mainloop,
+      so the publish does not wait for this tile's stores;
+    * the stored values (columns beyond N: the op's identity) are combined
+      per wave by ``mt_wave_row_reduce``, then over the ``sg_N`` waves that
+      share rows through LDS ``row_red`` in wave order;
+    * the tile's row values go to the workspace after its flag words, at
+      row block ``blockIdx.z * tiles_m + tile_m0 / tile_M`` and column tile
+      ``tile_n0 / tile_N``; the tile becomes the pending one, published by the
+      next tile or by ``MatmulRowReduceFinishFragment`` after the last.
+
+    Flag word ``block`` counts the published tiles of the block; the
+    workgroup that completes it combines its tiles in column order.  The
+    workspace holds ``rr_workspace_bytes`` and at most MT_WS_HEAD - 1 row
+    blocks (the assembler checks).  ``MatmulRowReduceSetupFragment`` declares
+    the pending tile before the tile loop."""
+
+    config: MatmulConfig
+    op: str
+    red_name: str
+    value_expr: str | None = None
+    check: bool = False
+    lds_name: str = "row_red"
+    # the tile loop walks whole row blocks (PersistentTiles.row_blocks):
+    # lane t < tile_M carries row t's running value from tile to tile and
+    # writes it after the block's last tile -- no workspace, no publish
+    local: bool = False
+    name: str = "matmul_row_reduce_store"
+    kind: str = "store"
+
+    def render(self, ctx: CodegenContext) -> str:
+        t, cfg = self.config.tile, self.config
+        opi, ident = _RR_OPS[self.op]
+        M, N = cfg.M_dim_var, cfg.N_dim_var
+        value = self.value_expr.format(a0="acc[i][j][v]") if self.value_expr else "acc[i][j][v]"
+        guard = f"if (row < {M} && col < {N}) " if self.check else ""
+        keep_col = f"col < {N} ? mt_y : {ident}" if self.check else "mt_y"
+        keep = max(1, 16 * t.WM // 32)
+        tm, tn, sgn, rr = t.tile_M, t.tile_N, t.sg_N, self.lds_name
+        combine = _rr_combine(self.op)
+        if self.local:
+            if tm > t.num_threads:
+                raise ValueError("a local row reduction keeps one row per lane: tile_M <= lanes")
+            tail = [
+                f"    if (threadIdx.x < {tm}u) {{",
+                f"        float r = {rr}[0][threadIdx.x];",
+                *(f"        r = {combine('r', f'{rr}[{n}][threadIdx.x]')};" for n in range(1, sgn)),
+                f"        mt_rr_run = mt_rr_first ? r : {combine('mt_rr_run', 'r')};",
+                f"        if (mt_rr_last && tile_m0 + threadIdx.x < {M}) {self.red_name}[tile_m0 + threadIdx.x] = mt_rr_run;",
+                "    }",
+            ]
+        else:
+            tail = [
+                f"    mt_rr_pend = blockIdx.z * (({M} + {tm - 1}u) / {tm}u) + tile_m0 / {tm}u;",
+                "    mt_rr_pend_m0 = tile_m0;",
+                f"    float* mt_rr_part = mt_ws + MT_WS_HEAD + (size_t)mt_rr_pend * (({N} + {tn - 1}u) / {tn}u) * {tm}u;",
+                f"    for (unsigned t = threadIdx.x; t < {tm}u; t += {t.num_threads}u) {{",
+                f"        float r = {rr}[0][t];",
+                *(f"        r = {combine('r', f'{rr}[{n}][t]')};" for n in range(1, sgn)),
+                f"        mt_rr_part[(size_t)(tile_n0 / {tn}u) * {tm}u + t] = r;",
+                "    }",
+            ]
+        return "\n".join(
+            [
+                "" if self.local else _rr_finish_call(self, "if (mt_rr_pend != 0xffffffffu) "),
+                "#pragma unroll",
+                f"for (int i = 0; i < {t.WM}; ++i) {{",
+                "#pragma unroll",
+                f"    for (int j = 0; j < {t.WN}; ++j) {{",
+                "        const unsigned col = tile_n0 + wave_n0 + (unsigned)j * 32u + (lane & 31u);",
+                "#pragma unroll",
+                "        for (int v = 0; v < 16; ++v) {",
+                "            const unsigned row = tile_m0 + wave_m0 + (unsigned)i * 32u + mt_acc_row(v, lane);",
+                f"            const float mt_y = {value};",
+                f"            {guard}{cfg.c_buffer_name}[(size_t)row * {N} + col] = mt_y;",
+                f"            acc[i][j][v] = {keep_col};",
+                "        }",
+                "    }",
+                "}",
+                "{",
+                f"    float mt_rr_keep[{keep}];",
+                f"    mt_wave_row_reduce<{t.WM}, {t.WN}, {opi}>(acc, lane, mt_rr_keep);",
+                "#pragma unroll",
+                f"    for (int k = 0; k < {keep}; ++k)",
+                f"        {rr}[wave % {sgn}u][wave_m0 + mt_rr_row<{t.WM}>(lane, k)] = mt_rr_keep[k];",
+                "    __syncthreads();",
+                *tail,
+                "}",
+            ]
+        )
+
+    @property
+    def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
+        shape = rr_lds_shape(self.config.tile)
+        return (
+            TgmemAccess(self.lds_name, "write", _prod(shape), shape),
+            TgmemAccess(self.lds_name, "read", _prod(shape), shape),
+        )
+
+
+def _rr_finish_call(frag: "MatmulRowReduceStoreFragment", head: str) -> str:
+    t, cfg = frag.config.tile, frag.config
+    opi, _ = _RR_OPS[frag.op]
+    return (
+        f"{head}mt_rr_finish<{opi}, {t.tile_M}u, {t.num_threads}u>(mt_ws, mt_rr_pend, "
+        f"({cfg.N_dim_var} + {t.tile_N - 1}u) / {t.tile_N}u, mt_rr_pend_m0, {cfg.M_dim_var}, {frag.red_name}, "
+        f"reinterpret_cast<unsigned*>(&{frag.lds_name}[{t.sg_N}][0]));"
+    )
+
+
+@dataclass(frozen=True)
+class MatmulRowReduceSetupFragment:
+    """Declares the pending tile of the row-reduction epilogue (none yet),
+    or in the local form the running row value; placed before the tile
+    loop."""
+
+    local: bool = False
+    name: str = "matmul_row_reduce_setup"
+    kind: str = "compute"
+
+    def render(self, ctx: CodegenContext) -> str:
+        if self.local:
+            return "float mt_rr_run = 0.0f;  // this lane's row: the row block's value so far"
+        return "unsigned mt_rr_pend = 0xffffffffu, mt_rr_pend_m0 = 0u;  // row block of the unpublished tile"
+
+    @property
+    def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
+        return ()
+
+
+@dataclass(frozen=True)
+class MatmulRowReduceFinishFragment:
+    """Publishes the workgroup's last tile of the row-reduction epilogue;
+    placed after the tile loop (every workgroup has at least one tile)."""
+
+    store: MatmulRowReduceStoreFragment
+    name: str = "matmul_row_reduce_finish"
+    kind: str = "store"
+
+    def render(self, ctx: CodegenContext) -> str:
+        return _rr_finish_call(self.store, "if (mt_rr_pend != 0xffffffffu) ")
+
+    @property
+    def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
+        shape = rr_lds_shape(self.store.config.tile)
+        return (
+            TgmemAccess(self.store.lds_name, "write", _prod(shape), shape),
+            TgmemAccess(self.store.lds_name, "read", _prod(shape), shape),
+        )
+
+
+def _rr_combine(op: str):
+    fn = {"sum": "{a} + {b}", "max": "fmaxf({a}, {b})", "min": "fminf({a}, {b})", "product": "{a} * {b}"}[op]
+    return lambda a, b: fn.format(a=a, b=b)
+
+
+def rr_lds_shape(t: TileConfig) -> tuple[int, int]:
+    """LDS of the row-reduction epilogue: one row of tile_M values per wave
+    column, and one more row whose first word is the publish flag."""
+    return (t.sg_N + 1, t.tile_M)
+
+
+def rr_workspace_bytes(M: int, N: int, t: TileConfig, batch: int = 1) -> int:
+    """Workspace of the row-reduction epilogue: the flag words, then one
+    tile_M-value row per (program, row block, column tile)."""
+    blocks = batch * ((M + t.tile_M - 1) // t.tile_M)
+    return 4 * (STREAM_K_HEAD_WORDS + blocks * ((N + t.tile_N - 1) // t.tile_N) * t.tile_M)
+
+
+def rr_row_blocks(M: int, t: TileConfig, batch: int = 1) -> int:
+    return batch * ((M + t.tile_M - 1) // t.tile_M)
+
+
 @dataclass(frozen=True)
 class MatmulAccumToDevFragment:
     """Store raw accumulators to the output (reference name, aligned path)."""
@@ -703,6 +912,9 @@ __all__ = [
     "MatmulEpilogueStoreFragment",
     "MatmulMainloopFragment",
     "MatmulRegisterEpilogueFragment",
+    "MatmulRowReduceFinishFragment",
+    "MatmulRowReduceSetupFragment",
+    "MatmulRowReduceStoreFragment",
     "MatmulSetupFragment",
     "MatmulTileMappingFragment",
     "PersistentLoopEndFragment",

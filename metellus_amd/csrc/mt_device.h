@@ -32,6 +32,10 @@
 //   * mt_stream_k / mt_sk_*   stream-K schedule of a persistent matmul and the
 //                             workspace flags that hand split tiles' partial
 //                             sums to the workgroup finishing them
+//   * mt_wave_row_reduce / mt_rr_*
+//                             row reductions of a matmul's output tile in its
+//                             epilogue (lane exchanges, then per-tile values
+//                             combined by the last workgroup of a row block)
 //
 // All indices are unsigned 32-bit except global offsets (size_t).
 
@@ -900,4 +904,149 @@ MT_INLINE void mt_sk_wait(unsigned* flag, unsigned* error) {
         __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Row reduction of a matmul's output in its epilogue (the matmul -> reduction
+// epilogue extension): the kernel that writes Y = A @ B (+ a register
+// epilogue) also writes r[row] = op over Y[row][:], op one of sum (OP 0),
+// max (1), min (2), product (3) with the row-reduction kernels' combines.
+//
+// 1. A wave holds WM x WN blocks of 32x32 values in the MFMA layout (lane l:
+//    column l % 32 of each block, 16 rows per block, mt_acc_row).  Per lane,
+//    the WN blocks of each row are combined in block order: 16 WM values.
+// 2. Across the 32 lanes of each half-wave, halving exchanges over lane bits
+//    0, 1, 2, 3, 4: a lane keeps the half of its values its bit selects,
+//    sends the other half to the lane that differs in that bit and combines
+//    what it receives into what it keeps; once a lane holds one value, the
+//    remaining steps combine both lanes' values.  Lane l then holds
+//    MT_RR_KEEP(WM) values, value k for wave row mt_rr_row<WM>(l, k).  The
+//    low bits go first: their exchanges are the most numerous and DPP quad
+//    permutes serve them within the VALU op; bits 2-4 go through ds_swizzle.
+// 3. The waves that share rows combine through LDS in wave order, one value
+//    per row of the tile (generated code).
+// 4. Each tile publishes its row values in the workspace (after the
+//    MT_WS_HEAD flag words); the workgroup that publishes a row block's last
+//    tile combines the block's tiles in column order and writes r.
+// Every step has a fixed order, so results are reproducible; max and min
+// give the same values as the row-reduction kernel, sum and product round
+// differently (another summation order).
+// ---------------------------------------------------------------------------
+
+#define MT_RR_KEEP(WM) ((16 * (WM)) >= 32 ? (16 * (WM)) / 32 : 1)
+
+template <int OP>
+MT_INLINE float mt_rr_op(float a, float b) {
+    if constexpr (OP == 0) return a + b;
+    else if constexpr (OP == 1) return fmaxf(a, b);
+    else if constexpr (OP == 2) return fminf(a, b);
+    else return a * b;
+}
+
+// v from the lane whose index differs from this lane's in the bits of M
+// (M < 32): DPP quad permutes for 1 and 2, ds_swizzle in its bitmask mode
+// (and 0x1F, xor M within each 32 lanes) for 4, 8 and 16.
+template <unsigned M>
+MT_INLINE float mt_xor_lanes(float v) {
+    const int x = __float_as_int(v);
+    int y;
+    if constexpr (M == 1u)
+        y = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+    else if constexpr (M == 2u)
+        y = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+    else
+        y = __builtin_amdgcn_ds_swizzle(x, (int)((M << 10) | 0x1Fu));
+    return __int_as_float(y);
+}
+
+// Wave-tile row of value k that `lane` keeps after mt_wave_row_reduce<WM>.
+template <int WM>
+MT_HD unsigned mt_rr_row(unsigned lane, int k) {
+    unsigned idx = 0u, n = 16u * (unsigned)WM;
+    for (int b = 0; b <= 4; ++b) {
+        if (n > 1u) {
+            n >>= 1;
+            if ((lane >> b) & 1u) idx += n;
+        }
+    }
+    idx += (unsigned)k;
+    const unsigned i = idx >> 4, r = idx & 15u;
+    return 32u * i + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3u);
+}
+
+// One exchange step over lane bit M with N values per lane (N == 1: combine).
+template <unsigned M, int N, int OP>
+MT_INLINE void mt_rr_step(float* w, unsigned lane) {
+    if constexpr (N > 1) {
+        constexpr int H = N / 2;
+        const bool hi = (lane & M) != 0u;
+#pragma unroll
+        for (int k = 0; k < H; ++k) {
+            const float send = hi ? w[k] : w[k + H];
+            const float keep = hi ? w[k + H] : w[k];
+            w[k] = mt_rr_op<OP>(keep, mt_xor_lanes<M>(send));
+        }
+    } else {
+        w[0] = mt_rr_op<OP>(w[0], mt_xor_lanes<M>(w[0]));
+    }
+}
+
+template <int WM, int WN, int OP>
+MT_INLINE void mt_wave_row_reduce(const mt_f32x16 (&val)[WM][WN], unsigned lane, float (&out)[MT_RR_KEEP(WM)]) {
+    constexpr int V = 16 * WM;
+    float w[V];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float x = val[i][0][r];
+#pragma unroll
+            for (int j = 1; j < WN; ++j) x = mt_rr_op<OP>(x, val[i][j][r]);
+            w[16 * i + r] = x;
+        }
+    constexpr int N1 = V > 1 ? V / 2 : 1, N2 = N1 > 1 ? N1 / 2 : 1, N3 = N2 > 1 ? N2 / 2 : 1, N4 = N3 > 1 ? N3 / 2 : 1;
+    mt_rr_step<1u, V, OP>(w, lane);
+    mt_rr_step<2u, N1, OP>(w, lane);
+    mt_rr_step<4u, N2, OP>(w, lane);
+    mt_rr_step<8u, N3, OP>(w, lane);
+    mt_rr_step<16u, N4, OP>(w, lane);
+#pragma unroll
+    for (int k = 0; k < MT_RR_KEEP(WM); ++k) out[k] = w[k];
+}
+
+// Publish this workgroup's tile values of a row block: every wave's stores
+// complete, the workgroup meets, then lane 0 increments the block's counter
+// with one agent-scope acquire-release add (the release writes back the
+// XCD's L2; the acquire invalidates the caches before the combining loads).
+// Returns true in every lane of the workgroup that published the block's
+// last tile, which resets the counter to 0 for the next launch.
+MT_INLINE bool mt_rr_publish(unsigned* counter, unsigned tiles, unsigned* flag_lds) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        const unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1u == tiles;
+        if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag_lds = last ? 1u : 0u;
+    }
+    __syncthreads();
+    return *flag_lds != 0u;
+}
+
+// Publish row block `blk`'s tile values written by this workgroup (a tile
+// earlier: its stores completed long ago, so the publish's wait is short)
+// and, in the workgroup that completes the block, combine the block's `tn`
+// column tiles in order into out[m0 + t] for the rows below M.
+template <int OP, unsigned TM, unsigned NT>
+MT_INLINE void mt_rr_finish(float* ws, unsigned blk, unsigned tn, unsigned m0, unsigned M, float* out,
+                            unsigned* flag_lds) {
+    const float* part = ws + MT_WS_HEAD + (size_t)blk * tn * TM;
+    if (mt_rr_publish(reinterpret_cast<unsigned*>(ws) + blk, tn, flag_lds)) {
+        for (unsigned t = threadIdx.x; t < TM; t += NT) {
+            if (m0 + t >= M) continue;
+            float r = part[t];
+            for (unsigned n = 1u; n < tn; ++n) r = mt_rr_op<OP>(r, part[(size_t)n * TM + t]);
+            out[m0 + t] = r;
+        }
+    }
 }

@@ -18,6 +18,7 @@ _MATMUL = {
     FusionStrategy.MATMUL_EPILOGUE_TG,
     FusionStrategy.MATMUL_EPILOGUE_REGISTER,
     FusionStrategy.ELEMENTWISE_PROLOGUE_MATMUL,
+    FusionStrategy.MATMUL_REDUCTION_EPILOGUE,
 }
 _REDUCTION = {
     FusionStrategy.STANDALONE_REDUCTION,

@@ -31,6 +31,9 @@ class DecisionView:
     shared_a: bool = False
     prologues_a: tuple[tuple[ElementwiseOp, ...], ...] = ()
     prologues_b: tuple[tuple[ElementwiseOp, ...], ...] = ()
+    # MATMUL_REDUCTION_EPILOGUE: the last-axis reduction of the matmul's
+    # (epilogue) output computed in the same kernel
+    reduction: ReductionOp | None = None
 
 
 def trace_prologue(target_name: str, candidates: tuple[Op, ...]) -> tuple[ElementwiseOp, ...]:
@@ -119,6 +122,8 @@ def classify(vertex: Vertex) -> DecisionView:
 
     at = ops.index(anchor)
     pre, post = ops[:at], ops[at + 1 :]
+    if isinstance(anchor, MatmulOp) and post and isinstance(post[-1], ReductionOp):
+        return _classify_matmul_reduction(ops, anchor, pre, post)
     epilogue = tuple(op for op in post if isinstance(op, ElementwiseOp))
     if isinstance(anchor, MatmulOp):
         pro_a = trace_prologue(anchor.a.name, pre)
@@ -142,3 +147,26 @@ def classify(vertex: Vertex) -> DecisionView:
     else:
         strategy = FusionStrategy.STANDALONE_REDUCTION
     return DecisionView(strategy=strategy, anchor=anchor, prologue_a=pro, epilogue=epilogue, ops=ops)
+
+
+def _classify_matmul_reduction(ops, anchor: MatmulOp, pre, post) -> DecisionView:
+    """(Extension, ``fusion.MATMUL_REDUCTION_EPILOGUES``.)  A matmul, its
+    lane-agnostic register epilogue and a last-axis reduction of the
+    epilogue's output, in one kernel that writes both."""
+    from metellus_amd.orchestrator import fusion
+
+    red = post[-1]
+    epilogue = post[:-1]
+    out = epilogue[-1].out if epilogue else anchor.out
+    assert fusion.MATMUL_REDUCTION_EPILOGUES, "v0: a matmul vertex holds no reduction"
+    assert not pre and all(isinstance(op, ElementwiseOp) and is_lane_agnostic_pred(op) for op in epilogue), (
+        "matmul -> reduction epilogue: no prologue, lane-agnostic epilogue only"
+    )
+    assert red.input.name == out.name, "matmul -> reduction epilogue: the reduction reads the matmul's output"
+    return DecisionView(
+        strategy=FusionStrategy.MATMUL_REDUCTION_EPILOGUE,
+        anchor=anchor,
+        epilogue=tuple(epilogue),
+        reduction=red,
+        ops=ops,
+    )

@@ -24,10 +24,14 @@ import dataclasses
 
 from metellus_amd.compute.fragments import BarrierFragment, CodegenContext, lds_decl
 from metellus_amd.compute.matmul.config import (
+    NUM_CUS,
+    STREAM_K_MAX_WORKGROUPS,
     TileConfig,
+    ceil_div,
     grid_for,
     is_aligned_shape,
     persistent_workgroups,
+    resident_workgroups,
     select_tile_config,
     uses_stream_k,
 )
@@ -36,12 +40,18 @@ from metellus_amd.compute.matmul.matmul import (
     MatmulConfig,
     MatmulEpilogueStoreFragment,
     MatmulMainloopFragment,
+    MatmulRowReduceFinishFragment,
+    MatmulRowReduceSetupFragment,
+    MatmulRowReduceStoreFragment,
     MatmulSetupFragment,
     MatmulTileMappingFragment,
     PersistentLoopEndFragment,
     PersistentTiles,
     StreamKFixupFragment,
     ThreadIndexFragment,
+    rr_lds_shape,
+    rr_row_blocks,
+    rr_workspace_bytes,
     stream_k_workspace_bytes,
 )
 from metellus_amd.memory.memory import TgLoadFragment, dma_offsets_fit
@@ -241,6 +251,19 @@ def b_tile_for(tile: TileConfig, src_b: Tensor, K: int, N: int) -> TileConfig:
     return dataclasses.replace(tile, b_pad=3)
 
 
+def rr_local(M: int, N: int, tile: TileConfig, batch: int = 1) -> bool:
+    """The row-reduction epilogue completes rows inside one workgroup (row
+    blocks walked whole, ``PersistentTiles.row_blocks``) when a tile spans
+    the whole row, or when the row blocks fill at least one round of the
+    GPU's resident workgroups.  Otherwise (few, long rows) every tile runs
+    in parallel and the row blocks are combined across workgroups through
+    the workspace (an agent-scope release per tile: slower per tile, but
+    not limited to a few workgroups)."""
+    if ceil_div(N, tile.tile_N) == 1:
+        return True
+    return batch * ceil_div(M, tile.tile_M) >= NUM_CUS * resident_workgroups(tile)
+
+
 def assemble_matmul(decision: DecisionView, function_name: str | None, batch: int = 1) -> KernelGroup:
     anchor = decision.anchor
     assert isinstance(anchor, MatmulOp)
@@ -311,9 +334,14 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
     b_load = operand_load(name="load_B_tile", src=src_b, dst="B_tile", tile=tile, side="b",
                           M=M, K=K, N=N, aligned=aligned, prologue=pro_b)
     n_persistent = persistent_workgroups(M, N, tile, batch)
-    stream_k = uses_stream_k(M, K, N, tile, n_persistent, batch)
-    persistent = PersistentTiles(tile.tile_M, tile.tile_N, stream_k=stream_k, tile_K=tile.tile_K) \
-        if n_persistent else None
+    red = decision.reduction
+    # the row-reduction epilogue needs each tile whole in one workgroup
+    stream_k = red is None and uses_stream_k(M, K, N, tile, n_persistent, batch)
+    local_rr = red is not None and rr_local(M, N, tile, batch)
+    if local_rr:
+        n_persistent = min(ceil_div(M, tile.tile_M), max(1, NUM_CUS * resident_workgroups(tile) // batch))
+    persistent = PersistentTiles(tile.tile_M, tile.tile_N, stream_k=stream_k, tile_K=tile.tile_K,
+                                 row_blocks=local_rr) if n_persistent else None
     mainloop = MatmulMainloopFragment(
         tile_K=tile.tile_K,
         fragments=(a_load, b_load, BarrierFragment("inputs_ready"), MatmulComputeFragment(config),
@@ -323,8 +351,18 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         spread=load_spread(pro_a, pro_b),
         spread_dma=LOAD_SPREAD_DMA,
     )
-    store = MatmulEpilogueStoreFragment(config, value_expr=value_expr, check=not aligned)
+    if red is None:
+        store = MatmulEpilogueStoreFragment(config, value_expr=value_expr, check=not aligned)
+    else:
+        if not local_rr and rr_row_blocks(M, tile, batch) > STREAM_K_MAX_WORKGROUPS:
+            raise ValueError(
+                f"{red.out.name}: the row-reduction epilogue counts row blocks in the workspace's "
+                f"{STREAM_K_MAX_WORKGROUPS} flag words; {rr_row_blocks(M, tile, batch)} needed"
+            )
+        store = MatmulRowReduceStoreFragment(config, op=red.op, red_name=param_name(red.out.buffer_key),
+                                             value_expr=value_expr, check=not aligned, local=local_rr)
     fragments = (
+        *((MatmulRowReduceSetupFragment(local=local_rr),) if red is not None else ()),
         MatmulTileMappingFragment(persistent),
         ThreadIndexFragment(tile),
         MatmulSetupFragment(config),
@@ -332,20 +370,30 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         *((StreamKFixupFragment(config),) if stream_k else ()),
         store,
         *((PersistentLoopEndFragment(),) if persistent else ()),
+        *((MatmulRowReduceFinishFragment(store),) if red is not None and not local_rr else ()),
     )
+    red_keys = (red.out.buffer_key,) if red is not None else ()
+    decls = (lds_decl("A_tile", tile.a_tile_shape()), lds_decl("B_tile", tile.b_tile_shape()))
+    if red is not None:
+        workspace = 0 if local_rr else rr_workspace_bytes(M, N, tile, batch)
+        decls += (lds_decl("row_red", rr_lds_shape(tile)),)
+    else:
+        workspace = stream_k_workspace_bytes(tile.tile_M, tile.tile_N, n_persistent) if stream_k else 0
     ctx = CodegenContext(
         function_name=function_name or f"matmul_{anchor.out.name}_fused",
-        buffers=(*(input_param(k) for k in slots), output_param(out_key), *extras.buffers),
+        buffers=(*(input_param(k) for k in slots), output_param(out_key), *extras.buffers,
+                 *(output_param(k) for k in red_keys)),
         dims=("M", "K", "N"),
         tg_x=tile.tg_x,
         tg_y=1,
-        threadgroup_decls=(lds_decl("A_tile", tile.a_tile_shape()), lds_decl("B_tile", tile.b_tile_shape())),
+        threadgroup_decls=decls,
         helpers=tuple(helpers),
-        workspace_bytes=stream_k_workspace_bytes(tile.tile_M, tile.tile_N, n_persistent) if stream_k else 0,
+        workspace_bytes=workspace,
+        workspace_batched=red is not None,
     )
     return KernelGroup(
         kernel=Kernel(fragments=fragments, ctx=ctx),
-        bindings=(*slots, out_key, *extras.bindings),
+        bindings=(*slots, out_key, *extras.bindings, *red_keys),
         dims=(M, K, N),
         grid=(n_persistent, 1, 1) if n_persistent else grid_for(M, N, tile),
         threads=(tile.tg_x, 1, 1),

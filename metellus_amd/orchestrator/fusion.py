@@ -366,6 +366,42 @@ _PASSES = (
 )
 
 
+# Extension beyond the reference's rules, off by default: a last-axis
+# reduction of a matmul's output (after the matmul's lane-agnostic register
+# epilogue, with no prologue) is computed by the matmul's kernel, which
+# writes the matmul output and the reduction both.  C5's S = Q @ K^T * s and
+# m1 = max(S) become one kernel, so S is not read back for m1.  It runs on
+# the reference's saturated partition (the reference's passes never see a
+# vertex holding both), and the reduction vertex must be the reduction alone.
+MATMUL_REDUCTION_EPILOGUES = False
+_ROW_REDUCTIONS = ("sum", "max", "min", "product")
+
+
+def try_matmul_reduction_fuse(graph: Graph, blacklist: Blacklist) -> Graph | None:
+    """(Extension, ``MATMUL_REDUCTION_EPILOGUES``.)  A vertex holding one
+    reduction whose input is the last output of a vertex holding one matmul
+    as its first op and lane-agnostic elementwise ops after it."""
+    if not MATMUL_REDUCTION_EPILOGUES:
+        return None
+    for r in graph.vertices:
+        if len(r.ops) != 1 or not isinstance(r.ops[0], ReductionOp) or r.ops[0].op not in _ROW_REDUCTIONS:
+            continue
+        red = r.ops[0]
+        a = graph.producer_of(red.input.name)
+        if a is None or a is r or not isinstance(a.ops[0], MatmulOp) or a.ops[-1].out.name != red.input.name:
+            continue
+        if not all(isinstance(op, ElementwiseOp) and _is_lane_agnostic(op) for op in a.ops[1:]):
+            continue
+        if (a.op_ids | r.op_ids) in blacklist:
+            continue
+        return graph.replace(absorbed=(a, r), ops=_by_position(graph, (*a.ops, *r.ops)))
+    return None
+
+
+# Extension passes, tried in order on the reference's saturated partition.
+_LATE_PASSES = (try_matmul_reduction_fuse,)
+
+
 # ---------------------------------------------------------------------------
 # Budget gate and driver (reference: fusion.py:443-545)
 # ---------------------------------------------------------------------------
@@ -415,17 +451,19 @@ def _modified_signature(old: Graph, new: Graph) -> frozenset[int]:
 def _fuse_once(program: Program, blacklist: Blacklist) -> tuple[tuple[Vertex, ...], frozenset[int] | None]:
     graph = Graph.from_program(program)
     _check_primitive_budgets(graph)
-    while True:
-        for rewrite in _PASSES:
-            candidate = rewrite(graph, blacklist)
-            if candidate is None:
-                continue
-            if not _fits_budget(graph, candidate):
-                return candidate.topo_sort(), _modified_signature(graph, candidate)
-            graph = candidate
-            break
-        else:
-            return graph.topo_sort(), None
+    for passes in (_PASSES, _LATE_PASSES):
+        while True:
+            for rewrite in passes:
+                candidate = rewrite(graph, blacklist)
+                if candidate is None:
+                    continue
+                if not _fits_budget(graph, candidate):
+                    return candidate.topo_sort(), _modified_signature(graph, candidate)
+                graph = candidate
+                break
+            else:
+                break
+    return graph.topo_sort(), None
 
 
 def fuse(program: Program) -> tuple[Vertex, ...]:

@@ -25,6 +25,9 @@ class FusionStrategy(str, Enum):
     STANDALONE_SHAPE = "standalone_shape"
     MULTI_PRODUCER_CONVERGENT = "multi_producer_convergent"
     DIAMOND_SHARED = "diamond_shared"
+    # extension (fusion.MATMUL_REDUCTION_EPILOGUES): a matmul whose output
+    # also feeds a last-axis reduction computed in the same kernel
+    MATMUL_REDUCTION_EPILOGUE = "matmul_reduction_epilogue"
 
     def __str__(self) -> str:
         return self.value

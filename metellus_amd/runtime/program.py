@@ -157,7 +157,7 @@ class Kernel:
         (launch with grid z = batch size)."""
         if self.ctx.batched:
             return self
-        if self.ctx.workspace_bytes:
+        if self.ctx.workspace_bytes and not self.ctx.workspace_batched:
             raise ValueError(f"{self.function_name}: a kernel with a workspace (stream-K) is not batched")
         cached = getattr(self, "_batched", None)
         if cached is None:
