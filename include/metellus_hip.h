@@ -121,7 +121,8 @@ int mt_launch(uint64_t kernel, const uint64_t* buffers, int nbuf, const uint32_t
  * it is for callers that cannot allocate device memory -- code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * Same parameters and kernel-parameter order as mt_launch, without timing;
- * when scratch_bytes > 0 (a stream-K kernel's workspace_bytes) the kernel's
+ * when scratch_bytes > 0 (the workspace_bytes of a stream-K kernel or of a
+ * row-reduction epilogue that combines row blocks across workgroups) the kernel's
  * last parameter is the library's static device scratch instead of the
  * mt_workspace buffer.  The scratch holds at most 64 MiB + 4096 bytes
  * (larger requests fail with an error and launch nothing); its 4096-byte

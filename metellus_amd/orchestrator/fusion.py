@@ -13,10 +13,15 @@ the top, until nothing fires ("saturation"):
 4. ``try_prologue_absorb_single`` elem -> anchor input (unique consumer)
 5. ``try_prologue_absorb_multi``  lane-agnostic elem recomputed in 2+ anchors
 
-An extension beyond the reference, off by default
-(``MULTI_ANCHOR_MERGE_CHAINS``), runs between 1 and 2:
-``try_multi_producer_chain_fuse`` merges two matmuls through a chain of
-elementwise ops instead of one (the MLP gate ``silu(X @ W1) * (X @ W2)``).
+Two extensions beyond the reference, off by default:
+
+* ``MULTI_ANCHOR_MERGE_CHAINS``: ``try_multi_producer_chain_fuse`` runs
+  between 1 and 2 and merges two matmuls through a chain of elementwise ops
+  instead of one (the MLP gate ``silu(X @ W1) * (X @ W2)``);
+* ``MATMUL_REDUCTION_EPILOGUES``: once the passes above are saturated,
+  ``try_matmul_reduction_fuse`` (the only late pass) joins a last-axis
+  reduction to the matmul vertex producing its input (attention's
+  ``max(Q @ K^T * s)``), so the reference's passes never see that vertex.
 
 Budget gate: each rewrite's new vertices are assembled and their LDS plan
 measured; a rewrite that exceeds the cap is blacklisted by its op-id
