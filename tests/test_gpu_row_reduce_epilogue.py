@@ -54,22 +54,19 @@ def _check_rows(op: str, r: np.ndarray, yc: np.ndarray) -> None:
         assert np.all(np.isfinite(ref)) and np.all(np.abs(r / ref - 1.0) <= 64 * EPS * yc.shape[1] ** 0.5)
 
 
-@pytest.mark.parametrize("op", ["max", "min", "sum", "product"])
-@pytest.mark.parametrize(
-    "shape",
-    [
-        (512, 64, 1024),  # one round of tiles
-        (300, 70, 520),  # ragged: bounds-checked loads, masked columns and rows
-        (4096, 128, 8192),  # 512 tiles: persistent workgroups
-    ],
-)
+_CASES = [
+    (op, shape)
+    for shape in ((512, 64, 1024), (300, 70, 520))  # one round of tiles; ragged (bounds, masked columns and rows)
+    for op in ("max", "min", "sum", "product")
+] + [("max", (4096, 128, 8192)), ("sum", (4096, 128, 8192))]  # 512 tiles: persistent workgroups
+
+
+@pytest.mark.parametrize("op,shape", _CASES)
 def test_fused_row_reduction(op, shape, monkeypatch):
     """Both forms -- row blocks combined across workgroups through the
     workspace, and row blocks walked whole by one workgroup -- on every
     shape (the assembler picks one by the number of row blocks; here each
     is forced); they combine in the same order, so they agree bit for bit."""
-    if shape == (4096, 128, 8192) and op in ("min", "product"):
-        pytest.skip("the persistent shape is covered by max and sum")
     monkeypatch.setattr(fusion, "MATMUL_REDUCTION_EPILOGUES", False)
     ref = run(_program(op, *shape), outputs=("Yc", "r", "z"))
     monkeypatch.setattr(fusion, "MATMUL_REDUCTION_EPILOGUES", True)
