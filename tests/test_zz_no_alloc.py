@@ -4,9 +4,10 @@ kernels (the kernels that use a scratch buffer) give bit-identical outputs
 from both entry points, on consecutive calls that shrink -- C4's X @ W1 at
 its full size with the real resident capacity (the whole 64 MiB of partial
 tiles), then smaller forced-capacity matmuls and a diamond with two
-accumulator sets, whose calls reuse the same scratch.  The scratch error
-word stays 0, and a request beyond the scratch's size is refused before
-anything is launched."""
+accumulator sets, whose calls reuse the same scratch; and the matmul ->
+reduction epilogue extension in its workspace form (row-block counters in
+the scratch's flag words).  The scratch error word stays 0, and a request
+beyond the scratch's size is refused before anything is launched."""
 
 from __future__ import annotations
 
@@ -97,3 +98,54 @@ def test_noalloc_refuses_oversized_scratch(monkeypatch):
     with pytest.raises(RuntimeError, match="static scratch holds"):
         hip_backend.launch_noalloc(g.kernel.handle, bufs, g.dims, g.kernel.dims_slot_index, g.grid, g.threads,
                                    scratch=SCRATCH_MAX + 4)
+
+
+def _row_max_program(M: int, K: int, N: int, seed: int) -> Operations:
+    rng = np.random.default_rng(seed)
+    ops = Operations()
+    ops.from_numpy(rng.standard_normal((M, K)).astype(np.float32), "A")
+    ops.from_numpy(rng.standard_normal((K, N)).astype(np.float32), "B")
+    ops.matmul(a="A", b="B", out="Y")
+    ops.elementwise("mul", out="Yc", operands=("Y", 0.5))
+    ops.reduction("max", out="r", x="Yc")
+    return ops
+
+
+def test_noalloc_runs_the_row_reduction_epilogue(monkeypatch):
+    """The matmul -> reduction epilogue in its workspace form (row blocks
+    combined across workgroups through counters in the flag words) from both
+    entry points, on two calls in a row, the second smaller: the same matmul
+    output and row maxima."""
+    from metellus_amd.orchestrator import fusion
+
+    hip_backend.init()
+    monkeypatch.setattr(fusion, "MATMUL_REDUCTION_EPILOGUES", True)
+    for shape, seed in (((512, 64, 1024), 41), ((300, 70, 520), 42)):
+        print(f"noalloc: row max epilogue {shape}", flush=True)
+        ops = _row_max_program(*shape, seed)
+        (g,) = compile_program(ops)
+        ws = g.kernel.workspace_bytes
+        assert 0 < ws <= SCRATCH_MAX and "mt_rr_finish<" in g.kernel.source.split('extern "C"')[-1]
+        inputs = {k: Buffer.from_numpy(a) for k, a in ops.uploads.items()}
+        got = []
+        for noalloc in (False, True):
+            outs = {k: Buffer(ops.tensors[k].nbytes) for k in g.bindings if k not in inputs}
+            for b in outs.values():
+                b.fill(0xFF)  # NaN pattern: every element must be written
+            bufs = [inputs[k] if k in inputs else outs[k] for k in g.bindings]
+            args = (g.kernel.handle, bufs, g.dims, g.kernel.dims_slot_index, g.grid, g.threads)
+            if noalloc:
+                assert hip_backend.launch_noalloc(*args, scratch=ws) == 0
+            else:
+                hip_backend.launch(*args, workspace=ws)
+                hip_backend.check_workspace()
+            got.append({k: b.numpy(ops.tensors[k].shape, np.float32) for k, b in outs.items()})
+            for b in outs.values():
+                b.release()
+        for b in inputs.values():
+            b.release()
+        a, b = got
+        assert not np.isnan(a["r"]).any() and not np.isnan(a["Yc"]).any()
+        for k in a:
+            np.testing.assert_array_equal(a[k], b[k])
+        np.testing.assert_array_equal(a["r"], a["Yc"].max(axis=1))
