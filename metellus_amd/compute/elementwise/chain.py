@@ -107,6 +107,9 @@ def _sum(a: str, b: str) -> str:
 
 
 FAST_DIVISION = {"div": "mt_div_fast(x, y)", "recip": "mt_div_fast(1.0f, x)"}
+# The same divisions when the divisor is known to be plain (mt_div_plain):
+# mt_div_fast's own first path, with no test.
+PLAIN_DIVISION = {"div": "(x) * mt_div_rcp(y)", "recip": "mt_div_rcp(x)"}
 
 
 @dataclass
@@ -172,7 +175,10 @@ class ChainCode:
     def arity(self) -> int:
         return len(self.seeds) + len(self.externals)
 
-    def helper(self) -> str:
+    def helper(self, plain: bool = False) -> str:
+        """The chain as a device function ``name(s..., e...)``.  ``plain``:
+        ``name_plain``, its divisions reduced to x * mt_div_rcp(y), exact
+        when every divisor is plain (``plain_divisors``)."""
         params = [f"float s{k}" for k in range(len(self.seeds))]
         params += [f"float e{k}" for k in range(len(self.externals))]
         local: dict[str, str] = {name: f"s{k}" for k, name in enumerate(self.seeds)}
@@ -194,17 +200,50 @@ class ChainCode:
                     subs[ph] = f"({local[o.name]})"
             template = elementwise_expression(op.op)
             if self.fast_div and op.op in FAST_DIVISION:
-                template = FAST_DIVISION[op.op]
+                template = (PLAIN_DIVISION if plain else FAST_DIVISION)[op.op]
             expr = wrap_bool(op.op, substitute(template, **subs))
             lines.append(f"    const float v{i} = {expr};")
             cur = f"v{i}"
             local[op.out.name] = cur
         body = "\n".join(lines)
         result = cur if cur is not None else "0.0f"
+        name = f"{self.name}_plain" if plain else self.name
         return (
-            f"__device__ __forceinline__ float {self.name}({', '.join(params)}) {{\n"
+            f"__device__ __forceinline__ float {name}({', '.join(params)}) {{\n"
             f"{body}\n    return {result};\n}}"
         )
+
+    def plain_divisors(self) -> list[int] | None:
+        """Indices k of the gathered operands e_k that are the divisors of the
+        chain's fast divisions, when every such divisor is one (then whether
+        they are plain is known from the gathered values alone); None when
+        the chain has no fast division or one divides by anything else."""
+        if not self.fast_div:
+            return None
+        ks: list[int] = []
+        for i, op in enumerate(self.chain):
+            if op.op not in FAST_DIVISION:
+                continue
+            if op.op == "recip" or (i, 1) not in self._operand_ext:
+                return None
+            ks.append(self._operand_ext[(i, 1)])
+        return sorted(set(ks)) or None
+
+    def helpers(self) -> list[str]:
+        """The helper, and its plain form when ``plain_divisors`` applies."""
+        return [self.helper(), *([self.helper(plain=True)] if self.plain_divisors() else [])]
+
+    def plain_apply_lambda(self) -> str:
+        """``apply_lambda`` calling the plain helper."""
+        n = len(self.externals)
+        args = ", ".join(["raw", *(f"e.v[{k}]" for k in range(n))])
+        return f"[=](float raw, const mt_vals<{n}>& e) -> float {{ return {self.name}_plain({args}); }}"
+
+    def plain_predicate_lambda(self) -> str:
+        """``[=](const mt_vals<E>& e) -> bool``: every divisor plain."""
+        n = len(self.externals)
+        test = " && ".join(f"mt_div_plain(e.v[{k}])" for k in self.plain_divisors())
+        return f"[=](const mt_vals<{n}>& e) -> bool {{ return {test}; }}"
 
     def call(self, seed_values: list[str], ext_values: list[str]) -> str:
         return f"{self.name}({', '.join([*seed_values, *ext_values])})"

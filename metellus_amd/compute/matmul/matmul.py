@@ -452,6 +452,23 @@ class MatmulMainloopFragment:
             return self._render_persistent(loads, computes, body)
         sync = self._sync(loads)
         spread = self._spread(loads)
+        # loaders whose divisors are fixed for the tile: tested once
+        plain_lds = [ld for ld in loads if getattr(ld, "plain_invariant", False)]
+
+        def loop(plain: bool | None) -> list[str]:
+            return [
+                "for (unsigned kt = 0; kt < n_chunks; ++kt) {",
+                "    const unsigned cur = kt & 1u;",
+                "    const bool more = kt + 1u < n_chunks;",
+                *self._next_loads(loads, spread, persistent=False),
+                *[f"    {c.render_stage('cur', 'mt_hook' if spread and i == 0 else None)}" for i, c in enumerate(computes)],
+                *_guarded("    if (more) {",
+                          [f"        {c}" for c in _nonempty(
+                              ld.render_commit("cur ^ 1u", plain=plain if ld in plain_lds else None) for ld in loads)]),
+                *[f"    {x}" for x in sync],
+                "}",
+            ]
+
         body += [
             f"const unsigned n_chunks = ({kvar} + {tk - 1}u) / {tk}u;",
             "{",
@@ -460,15 +477,21 @@ class MatmulMainloopFragment:
             "}",
             *_nonempty(ld.render_commit("0") for ld in loads),
             *sync,
-            "for (unsigned kt = 0; kt < n_chunks; ++kt) {",
-            "    const unsigned cur = kt & 1u;",
-            "    const bool more = kt + 1u < n_chunks;",
-            *self._next_loads(loads, spread, persistent=False),
-            *[f"    {c.render_stage('cur', 'mt_hook' if spread and i == 0 else None)}" for i, c in enumerate(computes)],
-            *_guarded("    if (more) {", [f"        {c}" for c in _nonempty(ld.render_commit("cur ^ 1u") for ld in loads)]),
-            *[f"    {x}" for x in sync],
-            "}",
         ]
+        if plain_lds:
+            # the tile's divisors are known after its first chunk: one test,
+            # then a k loop whose commits carry no per-element branch (or the
+            # same loop with the full chain)
+            body += [
+                "const bool mt_plain = " + " && ".join(ld.render_plain_test() for ld in plain_lds) + ";",
+                "if (mt_plain) {",
+                *[f"    {x}" for x in loop(True)],
+                "} else {",
+                *[f"    {x}" for x in loop(False)],
+                "}",
+            ]
+        else:
+            body += loop(None)
         return "{\n" + textwrap.indent("\n".join(body), "    ") + "\n}"
 
     def _spread(self, loads) -> int:

@@ -83,12 +83,22 @@ MT_INLINE void mt_st4_wt(float* p, mt_f32x4 v) {
 //     of 2^125 and beyond on the second path): the IEEE division.
 // Measured on the C5 P.V kernel (one division per A element): 296 us with
 // the correction on every element, 276 us with the product alone.
+// The two pieces that depend on y alone: the refined reciprocal, and whether
+// x * r is the whole quotient (mt_div_plain).  A loader whose divisors are
+// all plain computes x * mt_div_rcp(y) directly (commit_apply_fast).
+MT_INLINE float mt_div_rcp(float y) {
+    const float r = __builtin_amdgcn_rcpf(y);
+    return __builtin_fmaf(__builtin_fmaf(-y, r, 1.0f), r, r);
+}
+MT_INLINE bool mt_div_plain(float y) {
+    const float ay = __builtin_fabsf(y);
+    return ay >= 1.0f && ay < 0x1.0p+125f;
+}
 MT_INLINE float mt_div_fast(float x, float y) {
     const float ay = __builtin_fabsf(y);
-    float r = __builtin_amdgcn_rcpf(y);
-    r = __builtin_fmaf(__builtin_fmaf(-y, r, 1.0f), r, r);
+    const float r = mt_div_rcp(y);
     const float q = x * r;
-    if (__builtin_expect(ay >= 1.0f && ay < 0x1.0p+125f, 1)) return q;
+    if (__builtin_expect(mt_div_plain(y), 1)) return q;
     const float v = __builtin_fmaf(__builtin_fmaf(-q, y, x), r, q);
     const bool ok = ay > 0x1.0p-125f && ay < 1.0f && __builtin_fabsf(v) < 0x1.0p+125f;
     // The IEEE division stays on its (rarely taken) branch: the empty asm
@@ -466,6 +476,36 @@ struct mt_tile_colvec_g : mt_tile_colvec<ROWS, COLS, NT> {
         Base::template fetch<CHECK>(src, rs, row0, col0, rlim, clim, tid, mt_identity{}, q, Q);
     }
 
+    // True in every lane when P(e) holds for the gathered operands of every
+    // in-bounds slot of every lane of the wave (one wave-uniform test).
+    template <bool CHECK, typename P>
+    MT_INLINE bool all_plain(unsigned tid, P p) const {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned r = idx / CV, c = (idx % CV) * 4u;
+            const unsigned gr = this->r0 + r, gc = this->c0 + c;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < this->rl && gc < this->cl))) {
+#pragma unroll
+                for (int j = 0; j < NG; ++j) ok = ok && p(ex[i][j]);
+            }
+        }
+        return __builtin_amdgcn_ballot_w64(!ok) == 0ull;
+    }
+
+    // commit_apply with Q -- the chain with its divisions reduced to
+    // x * mt_div_rcp(y), exact when P holds -- when all_plain, without a
+    // branch per element; A otherwise.
+    template <int LD, bool CHECK, typename A, typename Q, typename P>
+    MT_INLINE void commit_apply_fast(float* lds, unsigned tid, A a, Q q, P p) {
+        if (__builtin_expect(all_plain<CHECK>(tid, p), 1)) {
+            commit_apply<LD, CHECK>(lds, tid, q);
+        } else {
+            commit_apply<LD, CHECK>(lds, tid, a);
+        }
+    }
+
     template <int LD, bool CHECK, typename A>
     MT_INLINE void commit_apply(float* lds, unsigned tid, A a) {
 #pragma unroll
@@ -519,6 +559,36 @@ struct mt_tile_rowvec_g : mt_tile_rowvec<ROWS, COLS, NT> {
         static_assert(SLOT, "only per-slot gathers are invariant along k");
         this->r0 = row0, this->c0 = col0, this->rl = rlim, this->cl = clim;
         Base::template fetch<CHECK>(src, cs, row0, col0, rlim, clim, tid, mt_identity{}, q, Q);
+    }
+
+    // True in every lane when P(e) holds for the gathered operands of every
+    // in-bounds slot of every lane of the wave (one wave-uniform test).
+    template <bool CHECK, typename P>
+    MT_INLINE bool all_plain(unsigned tid, P p) const {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned idx = tid + i * NT;
+            const unsigned c = idx / RV, r = (idx % RV) * 4u;
+            const unsigned gr = this->r0 + r, gc = this->c0 + c;
+            if ((TOTAL % NT == 0 || idx < (unsigned)TOTAL) && (!CHECK || (gr < this->rl && gc < this->cl))) {
+#pragma unroll
+                for (int j = 0; j < NG; ++j) ok = ok && p(ex[i][j]);
+            }
+        }
+        return __builtin_amdgcn_ballot_w64(!ok) == 0ull;
+    }
+
+    // commit_apply with Q -- the chain with its divisions reduced to
+    // x * mt_div_rcp(y), exact when P holds -- when all_plain, without a
+    // branch per element; A otherwise.
+    template <int LD, bool CHECK, typename A, typename Q, typename P>
+    MT_INLINE void commit_apply_fast(float* lds, unsigned tid, A a, Q q, P p) {
+        if (__builtin_expect(all_plain<CHECK>(tid, p), 1)) {
+            commit_apply<LD, CHECK>(lds, tid, q);
+        } else {
+            commit_apply<LD, CHECK>(lds, tid, a);
+        }
     }
 
     template <int LD, bool CHECK, typename A>

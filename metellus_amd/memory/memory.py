@@ -110,6 +110,12 @@ class TgLoadFragment:
     # tile needs the same ones: they are gathered with a tile's first chunk
     # and kept for the rest (``render_fetch(reuse=True)``: fetch_keep).
     gather_invariant: bool = False
+    # With gathering: the chain with its divisions reduced to x * 1/y
+    # (``plain_apply_lambda``) and the test that makes it exact
+    # (``plain_predicate``, over the gathered operands); the commit takes the
+    # plain chain when the whole wave passes (commit_apply_fast).
+    plain_apply_lambda: str | None = None
+    plain_predicate: str | None = None
     # mode "dma": direct-to-LDS loads (mt_tile_dma) of a row-major source
     # (row stride src_row_stride, unit column stride, every element in
     # bounds, no transform) into a dense tile of tile_shape; the fetch
@@ -198,10 +204,14 @@ class TgLoadFragment:
             if self.gather_invariant and not self.gather_per_slot:
                 raise ValueError(f"{self.name}: k-invariant gathers are per-slot gathers")
             slot = ", true" if self.gather_per_slot else ""
+            plain = ""
+            if self._plain_commit(mode):
+                plain = (f"\nconst auto xq_{self.dst_name} = {self.plain_apply_lambda};"
+                         f"\nconst auto xp_{self.dst_name} = {self.plain_predicate};")
             return (
                 f"{tmpl}_g<{rows}, {cols}, {self.num_threads}, {self.n_gathered}{slot}> {self.loader};\n"
                 f"const auto xg_{self.dst_name} = {self.gather_lambda};\n"
-                f"const auto xa_{self.dst_name} = {self.apply_lambda};"
+                f"const auto xa_{self.dst_name} = {self.apply_lambda};{plain}"
             )
         return f"{tmpl}<{rows}, {cols}, {self.num_threads}> {self.loader};\nconst auto {self.xform} = {self._lambda()};"
 
@@ -262,6 +272,20 @@ class TgLoadFragment:
             tail = ")" if deferred else f", {self.xform})"
         return f"{head}{strides}, {self.row_start}, {self.col_start}, {rlim}, {clim}, {tid}{tail};"
 
+    @property
+    def plain_invariant(self) -> bool:
+        """A plain chain whose divisors stay the same for every k-chunk of a
+        tile (k-invariant gathers): one test per tile decides its commits."""
+        return self.gathering and self.gather_invariant and self._plain_commit(self.resolved_mode())
+
+    def render_plain_test(self, tid: str = "threadIdx.x") -> str:
+        check = "true" if self.check else "false"
+        return f"{self.loader}.template all_plain<{check}>({tid}, xp_{self.dst_name})"
+
+    def _plain_commit(self, mode: str) -> bool:
+        """The commit tests for plain divisors (vectorised gather loaders)."""
+        return self.plain_apply_lambda is not None and self.plain_predicate is not None and mode in ("colvec", "rowvec")
+
     def _has_transform(self) -> bool:
         return self.transform_lambda is not None or self.value_transform is not None
 
@@ -270,14 +294,26 @@ class TgLoadFragment:
             return f"&{self.dst_name}[{stage}][0][0]"
         return f"&{self.dst_name}[0][0]"
 
-    def render_commit(self, stage: str = "0", tid: str = "threadIdx.x") -> str:
+    def render_commit(self, stage: str = "0", tid: str = "threadIdx.x", plain: bool | None = None) -> str:
+        """The commit to LDS stage ``stage``.  A loader with a plain chain
+        tests its divisors at each commit (``plain`` None), or takes the
+        plain (True) or the full chain (False) as its caller decided."""
         if self.is_dma:
             return ""
         if self.gathering:
             check = "true" if self.check else "false"
+            d = self.dst_name
+            if self._plain_commit(self.resolved_mode()):
+                if plain is None:
+                    return (
+                        f"{self.loader}.template commit_apply_fast<{self.pitch}, {check}>"
+                        f"({self.stage_ptr(stage)}, {tid}, xa_{d}, xq_{d}, xp_{d});"
+                    )
+                lam = f"xq_{d}" if plain else f"xa_{d}"
+                return f"{self.loader}.template commit_apply<{self.pitch}, {check}>({self.stage_ptr(stage)}, {tid}, {lam});"
             return (
                 f"{self.loader}.template commit_apply<{self.pitch}, {check}>"
-                f"({self.stage_ptr(stage)}, {tid}, xa_{self.dst_name});"
+                f"({self.stage_ptr(stage)}, {tid}, xa_{d});"
             )
         if self.defer_transform and self._has_transform() and self.resolved_mode() != "colvec_safe":
             check = "true" if self.check else "false"

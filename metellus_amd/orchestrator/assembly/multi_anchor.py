@@ -86,7 +86,7 @@ def assemble_multi_anchor(decision: DecisionView, function_name: str | None, bat
             return None
         code = ChainCode(tuple(chain), (src.name,), label, fast_div=_mm.FAST_DIV)
         code.register_extras(extras, base)
-        helpers.append(code.helper())
+        helpers.extend(code.helpers())
         return code
 
     tf_a = tuple(prologue(pro_a[i], src_a[i], f"prologue_a{i}") for i in range(2))

@@ -24,8 +24,13 @@ def test_broadcast_only_prologue_gathers_and_applies_at_commit():
     g = _by_name(compile_program(gpu_cases.attention_head(256, 64)))["matmul_O_fused"]
     src = g.kernel.source
     assert "mt_tile_colvec_g<" in src and "ld_A_tile.template fetch_gather<false>(" in src
-    assert "ld_A_tile.template commit_apply<" in src
-    assert "mt_div_fast(" in src.split('extern "C"')[0].split("prologue_a")[-1]
+    # the divisor is a gathered operand: the commit tests it once per wave and
+    # then divides as x * 1/y without a branch per element
+    assert "ld_A_tile.template commit_apply_fast<" in src
+    assert "xq_A_tile, xp_A_tile);" in src and "mt_div_plain(e.v[0])" in src
+    helpers = src.split('extern "C"')[0]
+    assert "mt_div_fast(" in helpers.split("float prologue_a(")[-1].split("}")[0]
+    assert "mt_div_rcp(" in helpers.split("float prologue_a_plain(")[-1].split("}")[0]
     assert "ld_B_tile.fetch(g_V, " in src  # no transform on V: loaded straight into LDS
     assert ", 32, " in src.split("mt_mfma_tile<")[-1].split(">")[0] + ", "
 
@@ -220,3 +225,26 @@ def test_k_invariant_gathers_are_loaded_once_per_tile(monkeypatch):
     # full-size gathered operands change with k: gathered with every chunk
     w3 = _by_name(compile_program(gpu_cases.mlp_block(256, 256, 512)))["matmul_out_fused"]
     assert "fetch_keep" not in w3.kernel.source.split('extern "C"')[1]
+
+
+def test_plain_divisors_only_for_gathered_divisors():
+    """The plain commit applies when every division of a prologue divides by
+    a gathered operand (known before the element); not for recip, not for a
+    divisor computed in the chain, not without fast division."""
+    from metellus_amd.compute.elementwise.chain import ChainCode
+    from metellus_amd.orchestrator.ir import ElementwiseOp, Scalar, Tensor
+
+    x, d, t = Tensor("x", (8, 8)), Tensor("d", (8, 8)), Tensor("t", (8, 8))
+    div = ElementwiseOp(out=Tensor("q", (8, 8)), op="div", operands=(x, d))
+    assert ChainCode((div,), ("x",), "p", fast_div=True).plain_divisors() == [0]
+    assert ChainCode((div,), ("x",), "p", fast_div=False).plain_divisors() is None
+    rec = ElementwiseOp(out=Tensor("r", (8, 8)), op="recip", operands=(x,))
+    assert ChainCode((rec,), ("x",), "p", fast_div=True).plain_divisors() is None
+    tt = ElementwiseOp(out=t, op="add", operands=(x, Scalar(1.0)))
+    inner = ElementwiseOp(out=Tensor("q2", (8, 8)), op="div", operands=(d, t))  # divides by a chain value
+    assert ChainCode((tt, inner), ("x",), "p", fast_div=True).plain_divisors() is None
+    mul = ElementwiseOp(out=Tensor("m", (8, 8)), op="mul", operands=(x, d))
+    assert ChainCode((mul,), ("x",), "p", fast_div=True).plain_divisors() is None
+    code = ChainCode((div,), ("x",), "p", fast_div=True)
+    assert code.plain_predicate_lambda() == "[=](const mt_vals<1>& e) -> bool { return mt_div_plain(e.v[0]); }"
+    assert "p_plain(" in code.helpers()[1] and "mt_div_rcp(" in code.helpers()[1]

@@ -116,3 +116,42 @@ def test_fused_epilogue_division_rounds_like_the_unfused_chain(op):
     tail(ew, "Cm")
     unfused = run(ew).env["Y"]
     np.testing.assert_array_equal(res.env["Y"], unfused)
+
+
+@pytest.mark.parametrize("divisors", ["plain", "some rows not plain"])
+def test_plain_commit_matches_per_element_division(divisors, monkeypatch):
+    """Y = (E / s[row]) @ V with the divisor gathered per row: the commit
+    that tests every divisor once per wave and then multiplies by 1/s
+    (``commit_apply_fast``) gives the bits of the per-element
+    ``mt_div_fast`` commit -- also when some rows' divisors (below 1, zero,
+    subnormal, infinite) send their waves down the per-element path."""
+    from metellus_amd.api import run
+    from metellus_amd.orchestrator import Operations
+    from metellus_amd.orchestrator.assembly import matmul as mm
+
+    rng = np.random.default_rng(41)
+    M, K, N = 512, 256, 128
+    e = rng.random((M, K), dtype=np.float32) + 0.1
+    s = (rng.random(M, dtype=np.float32) * 100.0 + 1.0).astype(np.float32)
+    if divisors != "plain":
+        s[[3, 77, 130, 400, 401]] = np.array([0.5, 0.0, 1e-40, np.inf, 2.0 ** 126], dtype=np.float32)
+    v = rng.standard_normal((K, N)).astype(np.float32)
+
+    def program():
+        ops = Operations()
+        ops.from_numpy(e, "E")
+        ops.from_numpy(s, "s")
+        ops.from_numpy(v, "V")
+        ops.reshape("s", (M, 1), out="sv")
+        ops.elementwise("div", out="P", operands=("E", "sv"), y_broadcast="col")
+        ops.matmul(a="P", b="V", out="Y")
+        return ops
+
+    outs = {}
+    for plain in (True, False):
+        monkeypatch.setattr(mm, "PLAIN_COMMIT", plain)
+        res = run(program(), outputs=("Y",))
+        src = res.groups[0].kernel.source.split('extern "C"')[-1]
+        assert ("commit_apply_fast<" in src) == plain
+        outs[plain] = res.env["Y"]
+    np.testing.assert_array_equal(outs[True], outs[False])
