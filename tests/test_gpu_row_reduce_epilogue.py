@@ -110,3 +110,55 @@ def test_attention_heads_batched(form, monkeypatch):
         for h in range(heads):
             for name in outs:
                 np.testing.assert_array_equal(got[h].env[name], ref[h].env[name], err_msg=f"head {h} {name}")
+
+
+_SIZES = (33, 64, 100, 130, 256, 257, 512, 768)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_matmul_row_reductions(seed, monkeypatch):
+    """Seeded random shapes (aligned and ragged), reductions and lane-agnostic
+    epilogues with the extension on: the matmul output is the reference
+    partition's, and the row values are the reduction of that output."""
+    rng = np.random.default_rng(1000 + seed)
+    M, K, N = (int(rng.choice(_SIZES)) for _ in range(3))
+    op = str(rng.choice(["max", "min", "sum", "product"]))
+    epi = [str(e) for e in rng.choice(["scale", "negate", "relu", "shift"], size=int(rng.integers(0, 3)))]
+
+    def program():
+        r = np.random.default_rng(seed)
+        ops = Operations()
+        ops.from_numpy(r.standard_normal((M, K)).astype(np.float32), "A")
+        ops.from_numpy((r.standard_normal((K, N)) / (4.0 * np.sqrt(K))).astype(np.float32), "B")
+        ops.matmul(a="A", b="B", out="Y")
+        cur = "Y"
+        for i, e in enumerate(epi):
+            nxt = f"E{i}"
+            if e == "scale":
+                ops.elementwise("mul", out=nxt, operands=(cur, 0.75))
+            elif e == "negate":
+                ops.elementwise("negate", out=nxt, operands=(cur,))
+            elif e == "relu":
+                ops.elementwise("max", out=nxt, operands=(cur, 0.0))
+            else:
+                ops.elementwise("add", out=nxt, operands=(cur, 1.0))
+            cur = nxt
+        if op == "product":  # values near 1 keep row products finite
+            ops.elementwise("mul", out="Pm", operands=(cur, 0.05))
+            ops.elementwise("add", out="Pa", operands=("Pm", 1.0))
+            cur = "Pa"
+        ops.reduction(op, out="r", x=cur)
+        ops.elementwise("mul", out="z", operands=(cur, 2.0))  # the matmul output stays a program value
+        return ops, cur
+
+    print(f"random row reduction {seed}: {op} {(M, K, N)} epilogue {epi}", flush=True)
+    ops_off, out = program()
+    monkeypatch.setattr(fusion, "MATMUL_REDUCTION_EPILOGUES", False)
+    ref = run(ops_off, outputs=(out, "r"))
+    monkeypatch.setattr(fusion, "MATMUL_REDUCTION_EPILOGUES", True)
+    res = run(program()[0], outputs=(out, "r"))
+    assert res.groups[0].strategy is FusionStrategy.MATMUL_REDUCTION_EPILOGUE
+    np.testing.assert_array_equal(res.env[out], ref.env[out])
+    _check_rows(op, res.env["r"], res.env[out])
+    if op in ("max", "min"):
+        np.testing.assert_array_equal(res.env["r"], ref.env["r"])
