@@ -164,10 +164,12 @@ GATHER_ONCE_PER_TILE = True  # k-invariant per-slot operands gathered with a til
 # epilogues and multi-anchor merges keep IEEE division.
 FAST_DIV = True
 # A gathering loader whose prologue divides only by gathered operands tests
-# them once per commit (every lane, every in-bounds slot: 1 <= |y| < 2^125)
-# and then applies the chain with x * 1/y and no per-element branch -- the
-# same bits as mt_div_fast.  Measured on MI355X, C5 P @ V, bit-identical:
-# 265.4 -> 259.3 us.
+# them (every lane, every in-bounds slot: 1 <= |y| < 2^125) and, when they
+# pass, applies the chain with x * 1/y and no per-element branch -- the same
+# bits as mt_div_fast.  Operands fixed for the tile (k-invariant gathers)
+# are tested once per tile and the k loop runs in one of two versions;
+# others are tested at each commit.  Measured on MI355X, C5 P @ V,
+# bit-identical: 262.3 -> 259.9 us (-2.2 % in GRBM_GUI_ACTIVE cycles).
 PLAIN_COMMIT = True
 
 
