@@ -333,10 +333,14 @@ class MatmulComputeFragment:
     name: str = "matmul_compute"
     kind: str = "compute"
 
-    def render_stage(self, stage: str | None, hook: str | None = None) -> str:
+    def render_stage(self, stage: str | None, hook: str | None = None,
+                     held: tuple[str, str] | None = None) -> str:
         """MFMAs over LDS buffer ``stage`` of double-buffered tiles, or over
         single-buffered tiles when ``stage`` is None; ``hook`` names a
-        callable run at each group of 4 k-steps (``mt_mfma_tile``)."""
+        callable run at each group of 4 k-steps (``mt_mfma_tile``).
+        ``held`` = (group variable, has-held expression): the chunk's last
+        group of 4 k-steps is carried to the next chunk
+        (``mt_mfma_tile_held``; no hook)."""
         t = self.config.tile
         at, bt = self.config.a_tile_name, self.config.b_tile_name
         a_ptr = f"&{at}[{stage}][wave_m0][0]" if stage is not None else f"&{at}[wave_m0][0]"
@@ -351,11 +355,29 @@ class MatmulComputeFragment:
             flags = f", {aswz}, {bnm}"
         if hook is not None and not flags:
             flags = ", false, false"
+        if held is not None:
+            if hook is not None:
+                raise ValueError("a held group and a load hook do not combine")
+            return (
+                f"mt_mfma_tile_held<{t.WM}, {t.WN}, {t.tile_K}, {t.lda}, {t.ldb}{flags}>"
+                f"({a_ptr}, {b_ptr}, acc{self.accumulator_suffix}, lane, {held[0]}, {held[1]});"
+            )
         hook_arg = f", {hook}" if hook is not None else ""
         return (
             f"mt_mfma_tile<{t.WM}, {t.WN}, {t.tile_K}, {t.lda}, {t.ldb}{flags}>"
             f"({a_ptr}, {b_ptr}, acc{self.accumulator_suffix}, lane{hook_arg});"
         )
+
+    def render_held_decl(self, var: str) -> str:
+        """Zeroed: after a k loop that ran no chunk its flush adds 0 * 0 to
+        accumulators that still hold +0."""
+        t = self.config.tile
+        return f"mt_mfma_group<{t.WM}, {t.WN}> {var} = {{}};"
+
+    def render_held_flush(self, var: str) -> str:
+        """The last chunk's held group, after the k loop."""
+        t = self.config.tile
+        return f"mt_mfma_group_run<{t.WM}, {t.WN}>({var}, acc{self.accumulator_suffix});"
 
     def render(self, ctx: CodegenContext) -> str:
         return self.render_stage("0" if self.config.tile.stages > 1 else None)
@@ -411,6 +433,9 @@ class MatmulMainloopFragment:
     # ``spread_dma``.
     spread: int = 0
     spread_dma: bool = False
+    # carry each chunk's last group of 4 k-steps over the barrier into the
+    # next chunk (``mt_mfma_tile_held``); not with spread loads
+    held: bool = False
     name: str = "matmul_mainloop"
     kind: str = "compute"
 
@@ -452,21 +477,24 @@ class MatmulMainloopFragment:
             return self._render_persistent(loads, computes, body)
         sync = self._sync(loads)
         spread = self._spread(loads)
+        held = self._held(spread)
         # loaders whose divisors are fixed for the tile: tested once
         plain_lds = [ld for ld in loads if getattr(ld, "plain_invariant", False)]
 
         def loop(plain: bool | None) -> list[str]:
             return [
+                *[c.render_held_decl(f"mt_held{i}") for i, c in enumerate(computes) if held],
                 "for (unsigned kt = 0; kt < n_chunks; ++kt) {",
                 "    const unsigned cur = kt & 1u;",
                 "    const bool more = kt + 1u < n_chunks;",
                 *self._next_loads(loads, spread, persistent=False),
-                *[f"    {c.render_stage('cur', 'mt_hook' if spread and i == 0 else None)}" for i, c in enumerate(computes)],
+                *self._computes_lines(computes, spread, held, "0u"),
                 *_guarded("    if (more) {",
                           [f"        {c}" for c in _nonempty(
                               ld.render_commit("cur ^ 1u", plain=plain if ld in plain_lds else None) for ld in loads)]),
                 *[f"    {x}" for x in sync],
                 "}",
+                *self._held_flush(computes, held),
             ]
 
         body += [
@@ -493,6 +521,25 @@ class MatmulMainloopFragment:
         else:
             body += loop(None)
         return "{\n" + textwrap.indent("\n".join(body), "    ") + "\n}"
+
+    def _held(self, spread: int) -> bool:
+        if self.held and spread:
+            raise ValueError("a held group and spread loads do not combine")
+        return self.held and self.tile_K >= 16
+
+    def _computes_lines(self, computes, spread: int, held: bool, k_begin: str) -> list[str]:
+        """The chunk's MFMAs: with a held group (carried when kt is not the
+        loop's first chunk), or with the spread loads' hook."""
+        if held:
+            return [f"    {c.render_stage('cur', held=(f'mt_held{i}', f'kt > {k_begin}'))}"
+                    for i, c in enumerate(computes)]
+        return [f"    {c.render_stage('cur', 'mt_hook' if spread and i == 0 else None)}" for i, c in enumerate(computes)]
+
+    @staticmethod
+    def _held_flush(computes, held: bool) -> list[str]:
+        """After the k loop: the last chunk's held group (a zeroed group when
+        the loop ran no chunk)."""
+        return [c.render_held_flush(f"mt_held{i}") for i, c in enumerate(computes)] if held else []
 
     def _spread(self, loads) -> int:
         """Hook points the next chunk's spread loads are issued at (0: none,
@@ -534,6 +581,7 @@ class MatmulMainloopFragment:
         tk = self.tile_K
         sync = self._sync(loads)
         spread = self._spread(loads)
+        held = self._held(spread)
         body += [
             "if (mt_first_tile) {",
             f"    const unsigned k_chunk = mt_kb * {tk}u;",
@@ -541,16 +589,18 @@ class MatmulMainloopFragment:
             *[f"    {c}" for c in _nonempty(ld.render_commit("mt_stage") for ld in loads)],
             *[f"    {x}" for x in sync],
             "}",
+            *[c.render_held_decl(f"mt_held{i}") for i, c in enumerate(computes) if held],
             "for (unsigned kt = mt_kb; kt < mt_ke; ++kt) {",
             "    const unsigned cur = mt_stage;",
             "    const bool more = kt + 1u < mt_ke;",
             *self._next_loads(loads, spread, persistent=True),
-            *[f"    {c.render_stage('cur', 'mt_hook' if spread and i == 0 else None)}" for i, c in enumerate(computes)],
+            *self._computes_lines(computes, spread, held, "mt_kb"),
             *_guarded("    if (more || mt_has_next) {",
                       [f"        {c}" for c in _nonempty(ld.render_commit("cur ^ 1u") for ld in loads)]),
             *[f"    {x}" for x in sync],
             "    mt_stage ^= 1u;",
             "}",
+            *self._held_flush(computes, held),
         ]
         return "{\n" + textwrap.indent("\n".join(body), "    ") + "\n}"
 

@@ -28,6 +28,8 @@
 //                             whose 16-byte slots are XOR-swizzled per row
 //   * mt_mfma_tile            fp32 MFMA (v_mfma_f32_32x32x2f32) over one LDS
 //                             k-chunk for a wave's WM x WN grid of 32x32 blocks
+//   * mt_mfma_tile_held       the same with the chunk's last group of 4 k-steps
+//                             carried over the barrier (mt_mfma_group)
 //   * mt_acc_row              row of accumulator register v in a 32x32 block
 //   * mt_stream_k / mt_sk_*   stream-K schedule of a persistent matmul and the
 //                             workspace flags that hand split tiles' partial
@@ -840,6 +842,87 @@ MT_INLINE void mt_mfma_tile(const float* __restrict__ As, const float* __restric
                 }
             }
         }
+    }
+    __builtin_amdgcn_s_setprio(0);
+}
+
+// ---------------------------------------------------------------------------
+// The same MFMAs with the chunk's last group of 4 k-steps carried over the
+// barrier.  A group's operands (4 k-steps of WM A and WN B fragments) are
+// read from LDS into a mt_mfma_group first; mt_mfma_tile_held reads group
+// g + 1 while group g's MFMAs run, and leaves the last group's operands in
+// `held`: the next chunk (or mt_mfma_group_run after the k loop) runs them
+// first, after the barrier, so the matrix core has work while the waves
+// leave the barrier and read the next chunk.  Per accumulator the products
+// are added in the same k order as mt_mfma_tile, so the results are
+// identical.  The barrier's release fence waits for the LDS reads into
+// `held` (lgkmcnt(0)) before another wave may overwrite the buffer.
+// ---------------------------------------------------------------------------
+
+template <int WM, int WN>
+struct mt_mfma_group {
+    mt_f32x4 a[WM];
+    mt_f32x4 b[WN];
+};
+
+template <int WM, int WN, int TK, int LDA, int LDB, bool ASWZ, bool BNM>
+MT_INLINE void mt_mfma_group_load(const float* __restrict__ As, const float* __restrict__ Bs, unsigned lane,
+                                  int s0, mt_mfma_group<WM, WN>& g) {
+    constexpr int HALF = TK / 2;
+    const unsigned li = lane & 31u;
+    const unsigned lh = lane >> 5;
+    unsigned m = 0u;
+    if constexpr (ASWZ || BNM) m = mt_swz<TK / 4>(li);
+    const float* a_base = ASWZ ? As + li * TK : As + li * LDA + lh * HALF;
+    const float* b_base = BNM ? Bs + li * TK : Bs + (lh * HALF) * LDB + li;
+    const unsigned slot = (lh * HALF + (unsigned)s0) / 4u;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+        g.a[i] = ASWZ ? mt_ld4(a_base + i * 32 * TK + 4u * (slot ^ m)) : mt_ld4(a_base + i * 32 * LDA + s0);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+        if constexpr (BNM) {
+            g.b[j] = mt_ld4(b_base + j * 32 * TK + 4u * (slot ^ m));
+        } else {
+#pragma unroll
+            for (int ss = 0; ss < 4; ++ss) g.b[j][ss] = b_base[(s0 + ss) * LDB + j * 32];
+        }
+    }
+}
+
+template <int WM, int WN>
+MT_INLINE void mt_mfma_group_run(const mt_mfma_group<WM, WN>& g, mt_f32x16 (&acc)[WM][WN]) {
+#pragma unroll
+    for (int ss = 0; ss < 4; ++ss)
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(g.a[i][ss], g.b[j][ss], acc[i][j], 0, 0, 0);
+}
+
+// Runs `held` (the previous chunk's last group) first when has_held, then
+// groups 0 .. G-2 of this chunk, and leaves group G-1's operands in `held`.
+template <int WM, int WN, int TK, int LDA, int LDB, bool ASWZ = false, bool BNM = false>
+MT_INLINE void mt_mfma_tile_held(const float* __restrict__ As, const float* __restrict__ Bs,
+                                 mt_f32x16 (&acc)[WM][WN], unsigned lane, mt_mfma_group<WM, WN>& held,
+                                 bool has_held) {
+    constexpr int G = TK / 8;
+    static_assert(TK % 8 == 0 && G >= 2, "a held group needs at least two groups of 4 k-steps per chunk");
+    static_assert(LDA % 4 == 0, "LDA must keep 16-byte alignment");
+    static_assert(!ASWZ || LDA == TK, "a swizzled A tile is dense");
+    static_assert(!BNM || LDB == TK, "an n-major B tile is dense");
+    __builtin_amdgcn_s_setprio(1);
+    mt_mfma_group<WM, WN> f[G - 1];
+    mt_mfma_group_load<WM, WN, TK, LDA, LDB, ASWZ, BNM>(As, Bs, lane, 0, f[0]);
+    if (has_held) mt_mfma_group_run<WM, WN>(held, acc);
+#pragma unroll
+    for (int g = 0; g < G - 1; ++g) {
+        if (g + 1 < G - 1)
+            mt_mfma_group_load<WM, WN, TK, LDA, LDB, ASWZ, BNM>(As, Bs, lane, 4 * (g + 1), f[g + 1]);
+        else
+            mt_mfma_group_load<WM, WN, TK, LDA, LDB, ASWZ, BNM>(As, Bs, lane, 4 * (g + 1), held);
+        mt_mfma_group_run<WM, WN>(f[g], acc);
     }
     __builtin_amdgcn_s_setprio(0);
 }

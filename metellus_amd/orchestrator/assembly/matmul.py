@@ -235,6 +235,21 @@ LOAD_SPREAD = 4
 LOAD_SPREAD_DMA = False  # spread direct-to-LDS loads too (measurements only)
 
 
+# Each chunk's last group of 4 k-steps carried over the barrier into the next
+# chunk (MatmulMainloopFragment.held) for mainloops of at least HELD_MIN_CHUNKS
+# chunks whose loads are not spread.  Measured on MI355X as shader-clock
+# cycles summed over the XCDs (GRBM_GUI_ACTIVE), bit-identical outputs:
+# 4096^3 -1.0 %, C4 X @ W1 -0.6 %, C5 P @ V -0.5 to -0.8 %; C5 Q @ K^T
+# (4 chunks) +3.0 % and C4 (h1*s*h2) @ W3 (spread loads, 236 VGPRs)
+# +8.6 %, which keep the plain mainloop.
+HELD_GROUPS = True
+HELD_MIN_CHUNKS = 16
+
+
+def held_groups(K: int, tile: TileConfig, spread: int) -> bool:
+    return HELD_GROUPS and not spread and tile.tile_K >= 16 and K >= HELD_MIN_CHUNKS * tile.tile_K
+
+
 def load_spread(*prologues: ChainCode | None) -> int:
     """Spread parts for a mainloop whose A / B prologues are ``prologues``."""
     return LOAD_SPREAD if any(gathers_full_operands(p) for p in prologues) else 0
@@ -352,14 +367,16 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         n_persistent = min(ceil_div(M, tile.tile_M), max(1, NUM_CUS * resident_workgroups(tile) // batch))
     persistent = PersistentTiles(tile.tile_M, tile.tile_N, stream_k=stream_k, tile_K=tile.tile_K,
                                  row_blocks=local_rr) if n_persistent else None
+    spread = load_spread(pro_a, pro_b)
     mainloop = MatmulMainloopFragment(
         tile_K=tile.tile_K,
         fragments=(a_load, b_load, BarrierFragment("inputs_ready"), MatmulComputeFragment(config),
                    BarrierFragment("compute_done")),
         K_dim_var="K",
         persistent=persistent is not None,
-        spread=load_spread(pro_a, pro_b),
+        spread=spread,
         spread_dma=LOAD_SPREAD_DMA,
+        held=held_groups(K, tile, spread),
     )
     if red is None:
         store = MatmulEpilogueStoreFragment(config, value_expr=value_expr, check=not aligned)
