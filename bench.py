@@ -949,7 +949,7 @@ def main() -> int:
     if args.gpus != 1 or world != 1:
         print(
             "bench.py: this build measures one MI355X; the path shards by rows / heads / output "
-            "tiles with no exchange (see DESIGN.md), and multi-GPU runs are not part of it. "
+            "tiles with no exchange, and multi-GPU runs are not part of it. "
             f"Requested --gpus {args.gpus} (WORLD_SIZE={world}).",
             file=sys.stderr,
         )
