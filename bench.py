@@ -334,19 +334,14 @@ def time_kernels(prep: Prepared, steps: int, warmup: int, flusher, label: str) -
 
 
 def check_c2(prep: Prepared) -> float:
-    """Max abs error of the GPU output on 64 sampled rows vs the oracle."""
-    from oracle.ir_eval import apply_elementwise
-
+    """Max abs error of the GPU output on 64 sampled rows against the chain
+    sigmoid(a*b + c) * d in NumPy float32 (the whole-output checks against
+    the oracle are GPU tests; this guards the timed run)."""
     out = prep.download("out", (4096, 4096))
     rows = np.random.default_rng(0).choice(4096, 64, replace=False)
     u = {k: prep.ops.uploads[k][rows] for k in "abcd"}
-    t = apply_elementwise("mul", u["a"], u["b"])
-    t = apply_elementwise("add", t, u["c"])
-    t = apply_elementwise("negate", t)
-    t = apply_elementwise("exp", t)
-    t = apply_elementwise("add", t, np.float32(1.0))
-    t = apply_elementwise("recip", t)
-    t = apply_elementwise("mul", t, u["d"])
+    one = np.float32(1.0)
+    t = one / (np.exp(-(u["a"] * u["b"] + u["c"])) + one) * u["d"]
     err = np.abs(out[rows] - t)
     tol = 1e-5 + 1e-5 * np.abs(t)
     if not np.all(err <= tol):
