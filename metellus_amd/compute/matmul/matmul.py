@@ -613,6 +613,126 @@ class MatmulMainloopFragment:
         return self.fragments
 
 
+@dataclass(frozen=True)
+class MatmulRowWavesFragment:
+    """A whole matmul 128 columns wide on row-owning waves (``mt_rw_*``):
+    256 x 128 tiles on 1024 lanes, 16 waves of 16 rows x 128 columns of
+    16x16x4 MFMAs.  A wave reads its own A rows from global memory into
+    registers, a 64-wide k-chunk ahead, and applies the prologue there
+    (``prologue``: None; ``("transform", lambda)`` over (raw, row, col); or
+    ``("gather", gather, apply, plain_apply, plain_predicate)`` with operands
+    fixed per row, read once per lane); B goes straight into two LDS stages
+    (``B_tile[2][64][128]``) by direct-to-LDS loads.  With a plain form of
+    the prologue, every lane tests its row's divisors once
+    (``__syncthreads_and``) and the workgroup runs the k loop with the plain
+    form when all pass.  Needs M % 256 == 0, N == 128, K % 128 == 0 (the
+    loop takes two chunks a trip).  The epilogue stores 128 bits per row;
+    ``value_expr`` is a format string over ``{a0}`` with ``row`` and ``col``
+    in scope."""
+
+    a_name: str
+    b_name: str
+    c_name: str
+    a_row_stride: int
+    b_row_stride: int
+    prologue: tuple | None = None
+    value_expr: str | None = None
+    name: str = "matmul_row_waves"
+    kind: str = "compute"
+
+    TILE_M = 256
+    TILE_N = 128
+    TILE_K = 64
+    THREADS = 1024
+
+    def _loop(self, pa: str) -> list[str]:
+        a, b, brs = self.a_name, self.b_name, self.b_row_stride
+        return [
+            "for (unsigned kt = 0; kt < n_chunks; kt += 2u) {",
+            "    mt_rw_load(mt_a1, mt_arow, (kt + 1u) * 64u);",
+            f"    ld_B.fetch({b}, {brs}, (kt + 1u) * 64u, 0u, &B_tile[1][0][0]);",
+            f"    mt_rw_chunk(mt_a0, &B_tile[0][0][0], {pa}, lane, acc);",
+            "    __builtin_amdgcn_s_waitcnt(0);",
+            "    __syncthreads();",
+            "    if (kt + 2u < n_chunks) {",
+            "        mt_rw_load(mt_a0, mt_arow, (kt + 2u) * 64u);",
+            f"        ld_B.fetch({b}, {brs}, (kt + 2u) * 64u, 0u, &B_tile[0][0][0]);",
+            "    }",
+            f"    mt_rw_chunk(mt_a1, &B_tile[1][0][0], {pa}, lane, acc);",
+            "    __builtin_amdgcn_s_waitcnt(0);",
+            "    __syncthreads();",
+            "}",
+        ]
+
+    def render(self, ctx: CodegenContext) -> str:
+        a, b, c = self.a_name, self.b_name, self.c_name
+        pro = self.prologue
+        lines = [
+            "const unsigned lane = mt_lane();",
+            "const unsigned wave = mt_wave();",
+            "const unsigned tile_m0 = blockIdx.y * 256u;",
+            "const unsigned mt_row = tile_m0 + wave * 16u + (lane & 15u);",
+            "mt_f32x4 acc[8];",
+            "#pragma unroll",
+            "for (int j = 0; j < 8; ++j) acc[j] = mt_f32x4{0.f, 0.f, 0.f, 0.f};",
+            f"const mt_tile_dma<64, 128, 1024, false> ld_B({self.b_row_stride}, threadIdx.x);",
+            f"const float* __restrict__ mt_arow = {a} + (size_t)mt_row * {self.a_row_stride}u + 16u * (lane >> 4);",
+            "mt_f32x4 mt_a0[4], mt_a1[4];",
+        ]
+        plain = False
+        if pro is None:
+            lines.append("const auto mt_pa = [](float raw) -> float { return raw; };")
+        elif pro[0] == "transform":
+            lines += [f"const auto xt = {pro[1]};",
+                      "const auto mt_pa = [=](float raw) -> float { return xt(raw, mt_row, 0u); };"]
+        else:
+            _, gather, apply, plain_apply, plain_pred = pro
+            lines += [f"const auto xg = {gather};", f"const auto xa = {apply};",
+                      "const auto mt_e = xg(mt_row, 0u);  // the row's operands",
+                      "const auto mt_pa = [=](float raw) -> float { return xa(raw, mt_e); };"]
+            if plain_apply is not None:
+                plain = True
+                lines += [f"const auto xq = {plain_apply};", f"const auto xp = {plain_pred};",
+                          "const auto mt_pq = [=](float raw) -> float { return xq(raw, mt_e); };"]
+        lines += [
+            "mt_rw_load(mt_a0, mt_arow, 0u);",
+            f"ld_B.fetch({b}, {self.b_row_stride}, 0u, 0u, &B_tile[0][0][0]);",
+            "__builtin_amdgcn_s_waitcnt(0);",
+            "__syncthreads();",
+            "const unsigned n_chunks = K / 64u;",
+        ]
+        if plain:
+            lines += ["if (__syncthreads_and(xp(mt_e) ? 1 : 0) != 0) {",
+                      *[f"    {x}" for x in self._loop("mt_pq")], "} else {",
+                      *[f"    {x}" for x in self._loop("mt_pa")], "}"]
+        else:
+            lines += self._loop("mt_pa")
+        value = self.value_expr.format(a0="acc[4 * h + j][i]") if self.value_expr else "acc[4 * h + j][i]"
+        lines += [
+            "#pragma unroll",
+            "for (int i = 0; i < 4; ++i) {",
+            "    const unsigned row = tile_m0 + wave * 16u + 4u * (lane >> 4) + (unsigned)i;",
+            "#pragma unroll",
+            "    for (int h = 0; h < 2; ++h) {",
+            "        const unsigned col0 = 64u * (unsigned)h + 4u * (lane & 15u);",
+            "        mt_f32x4 mt_o;",
+            "#pragma unroll",
+            "        for (int j = 0; j < 4; ++j) {",
+            "            const unsigned col = col0 + (unsigned)j;",
+            "            (void)col;",
+            f"            mt_o[j] = {value};",
+            "        }",
+            f"        *reinterpret_cast<mt_f32x4*>(&{c}[(size_t)row * N + col0]) = mt_o;",
+            "    }",
+            "}",
+        ]
+        return "{\n" + textwrap.indent("\n".join(lines), "    ") + "\n}"
+
+    @property
+    def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
+        return (TgmemAccess("B_tile", "read", 2 * 64 * 128, (2, 64, 128)),)
+
+
 def _nonempty(lines) -> list[str]:
     return [x for x in lines if x]
 
@@ -978,6 +1098,7 @@ class MatmulRegisterEpilogueFragment:
 
 __all__ = [
     "MatmulAccumToDevFragment",
+    "MatmulRowWavesFragment",
     "MatmulAccumToTgFragment",
     "MatmulTgToDevFragment",
     "MatmulComputeFragment",

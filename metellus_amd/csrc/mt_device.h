@@ -30,6 +30,8 @@
 //                             k-chunk for a wave's WM x WN grid of 32x32 blocks
 //   * mt_mfma_tile_held       the same with the chunk's last group of 4 k-steps
 //                             carried over the barrier (mt_mfma_group)
+//   * mt_rw_*                 row-owning waves for matmuls 128 columns wide
+//                             (16x16x4 MFMAs, A in registers, B in LDS)
 //   * mt_acc_row              row of accumulator register v in a 32x32 block
 //   * mt_stream_k / mt_sk_*   stream-K schedule of a persistent matmul and the
 //                             workspace flags that hand split tiles' partial
@@ -925,6 +927,77 @@ MT_INLINE void mt_mfma_tile_held(const float* __restrict__ As, const float* __re
         mt_mfma_group_run<WM, WN>(f[g], acc);
     }
     __builtin_amdgcn_s_setprio(0);
+}
+
+// ---------------------------------------------------------------------------
+// Row-owning waves for matmuls 128 columns wide.  Each of a workgroup's 16
+// waves owns 16 rows x all 128 columns of a 256 x 128 tile, computed with
+// v_mfma_f32_16x16x4f32 (D[16x16] += A[16x4] * B[4x16]; lane l supplies
+// A[l%16][l/16] and B[l/16][l%16] and holds D[4 (l/16) + i][l%16], i < 4).
+// A wave's A rows are its own: they go from global memory straight into the
+// registers the MFMAs take (a prologue applied there), and only B is staged
+// in LDS, as 64-wide k-chunks in two stages (64 KiB).
+//   k: lane group g = l/16 takes a chunk's columns 16 g .. 16 g + 15, one per
+//      step, so its A values are 16 consecutive floats (four 128-bit loads);
+//   n: column block j < 4 puts lane column c = l%16 at output column 4 c + j,
+//      block j >= 4 at 64 + 4 c + (j - 4), so a step's 8 B values are two
+//      128-bit LDS reads (256 contiguous bytes per 16 lanes, no bank
+//      conflicts) and each output row is stored 128 bits at a time.
+// ---------------------------------------------------------------------------
+
+struct mt_rw_group {
+    mt_f32x4 b[2][2];  // [step][column half]
+};
+
+MT_INLINE void mt_rw_group_load(mt_rw_group& g, const float* __restrict__ Bs, unsigned krow0, unsigned c) {
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) {
+        g.b[ss][0] = mt_ld4(Bs + (krow0 + (unsigned)ss) * 128u + 4u * c);
+        g.b[ss][1] = mt_ld4(Bs + (krow0 + (unsigned)ss) * 128u + 64u + 4u * c);
+    }
+}
+
+template <typename P>
+MT_INLINE void mt_rw_group_run(const mt_rw_group& g, float a0, float a1, P pa, mt_f32x4 (&acc)[8]) {
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) {
+        const float a = pa(ss == 0 ? a0 : a1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, g.b[ss][0][j], acc[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[4 + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, g.b[ss][1][j], acc[4 + j], 0, 0, 0);
+    }
+}
+
+// One 64-wide chunk from the B stage at Bs (rows of 128 floats) and this
+// lane's 16 A values `a` (raw; pa applies the prologue): 8 groups of 2
+// steps, each group's B values read while the previous group's MFMAs run
+// (the order pinned with sched_barrier: left alone, the compiler reads each
+// value just before its MFMA and waits for it there).
+template <typename P>
+MT_INLINE void mt_rw_chunk(const mt_f32x4 (&a)[4], const float* __restrict__ Bs, P pa, unsigned lane,
+                           mt_f32x4 (&acc)[8]) {
+    const unsigned c = lane & 15u;
+    const unsigned k0 = 16u * (lane >> 4);
+    __builtin_amdgcn_s_setprio(1);
+    mt_rw_group f[8];
+    mt_rw_group_load(f[0], Bs, k0, c);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        if (g + 1 < 8) mt_rw_group_load(f[g + 1], Bs, k0 + 2u * (unsigned)(g + 1), c);
+        __builtin_amdgcn_sched_barrier(0);
+        mt_rw_group_run(f[g], a[g / 2][2 * (g % 2)], a[g / 2][2 * (g % 2) + 1], pa, acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+}
+
+// This lane's A values of the chunk at k0: arow points at its row's column
+// 16 (lane / 16).
+MT_INLINE void mt_rw_load(mt_f32x4 (&a)[4], const float* __restrict__ arow, unsigned k0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = mt_ld4(arow + k0 + 4u * (unsigned)q);
 }
 
 // Row (within a 32x32 output block) of accumulator register v held by `lane`;

@@ -43,6 +43,7 @@ from metellus_amd.compute.matmul.matmul import (
     MatmulRowReduceFinishFragment,
     MatmulRowReduceSetupFragment,
     MatmulRowReduceStoreFragment,
+    MatmulRowWavesFragment,
     MatmulSetupFragment,
     MatmulTileMappingFragment,
     PersistentLoopEndFragment,
@@ -250,6 +251,37 @@ def held_groups(K: int, tile: TileConfig, spread: int) -> bool:
     return HELD_GROUPS and not spread and tile.tile_K >= 16 and K >= HELD_MIN_CHUNKS * tile.tile_K
 
 
+# Matmuls 128 columns wide (C5 P @ V) on row-owning waves
+# (MatmulRowWavesFragment): every wave owns 16 rows x 128 columns, so its A
+# rows go from global memory straight into its registers and only B is
+# staged in LDS, which leaves room for 64-wide k-chunks -- half the barriers
+# of the LDS-tiled kernel, whose 256 x 128 tiles give each wave only 32
+# MFMAs per 32-wide chunk.  Measured on MI355X, C5 P @ V (32 heads batched),
+# same run: 249.8 -> 253.1 us against 257.6 -> 261.5 us for the LDS-tiled
+# kernel (0.863-0.874 of the fp32 MFMA peak against 0.835-0.848); outputs
+# agree to rounding (another MFMA shape: 16x16x4 instead of 32x32x2).
+ROW_WAVES = True
+ROW_WAVES_MIN_K = 1024
+
+
+def row_waves(M: int, K: int, N: int, src_a: Tensor, src_b: Tensor, pro_a: ChainCode | None,
+              pro_b: ChainCode | None, reduction) -> bool:
+    """Whether a matmul takes the row-owning-wave kernel: 128 columns, whole
+    256-row tiles, whole pairs of 64-wide chunks and at least
+    ROW_WAVES_MIN_K of them, both operands read along rows with 16-byte
+    aligned rows, no B prologue, an A prologue whose operands are fixed per
+    row (or none), and no reduction epilogue."""
+    if not ROW_WAVES or reduction is not None or pro_b is not None:
+        return False
+    if N != 128 or M % 256 or K % 128 or K < ROW_WAVES_MIN_K:
+        return False
+    if src_a.col_stride != 1 or src_a.row_stride % 4 or src_b.col_stride != 1 or src_b.row_stride % 4:
+        return False
+    if not dma_offsets_fit(64, 128, src_b.row_stride):
+        return False
+    return pro_a is None or pro_a.external_axes() <= {"row"}
+
+
 def load_spread(*prologues: ChainCode | None) -> int:
     """Spread parts for a mainloop whose A / B prologues are ``prologues``."""
     return LOAD_SPREAD if any(gathers_full_operands(p) for p in prologues) else 0
@@ -323,6 +355,10 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         epi.register_extras(extras, base)
         helpers.append(epi.helper())
         value_expr = epi.scalar_call(["{a0}"], "row", "col")
+
+    if row_waves(M, K, N, src_a, src_b, pro_a, pro_b, decision.reduction):
+        return _assemble_row_waves(decision, function_name, src_a, src_b, pro_a, value_expr, slots, out_key,
+                                   extras, helpers, M, K, N)
 
     full_gather = gathers_full_operands(pro_a) or gathers_full_operands(pro_b)
     tile = b_tile_for(select_tile_config(M, K, N, batch=batch, wide=WIDE_TILES and not full_gather), src_b, K, N)
@@ -424,6 +460,48 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
         dims=(M, K, N),
         grid=(n_persistent, 1, 1) if n_persistent else grid_for(M, N, tile),
         threads=(tile.tg_x, 1, 1),
+        ops=decision.ops,
+        strategy=decision.strategy,
+    )
+
+
+def _assemble_row_waves(decision: DecisionView, function_name: str | None, src_a: Tensor, src_b: Tensor,
+                        pro_a: ChainCode | None, value_expr: str | None, slots: dict[str, int], out_key: str,
+                        extras: Extras, helpers: list[str], M: int, K: int, N: int) -> KernelGroup:
+    """The matmul as one MatmulRowWavesFragment (``row_waves`` holds)."""
+    prologue = None
+    if pro_a is not None:
+        if gathers(pro_a):
+            plain = PLAIN_COMMIT and pro_a.plain_divisors()
+            prologue = ("gather", pro_a.gather_lambda(), pro_a.apply_lambda(),
+                        pro_a.plain_apply_lambda() if plain else None,
+                        pro_a.plain_predicate_lambda() if plain else None)
+        else:
+            prologue = ("transform", pro_a.lambda_transform())
+    frag = MatmulRowWavesFragment(
+        a_name=param_name(src_a.buffer_key),
+        b_name=param_name(src_b.buffer_key),
+        c_name=param_name(out_key),
+        a_row_stride=src_a.row_stride,
+        b_row_stride=src_b.row_stride,
+        prologue=prologue,
+        value_expr=value_expr,
+    )
+    ctx = CodegenContext(
+        function_name=function_name or f"matmul_{decision.anchor.out.name}_fused",
+        buffers=(*(input_param(k) for k in slots), output_param(out_key), *extras.buffers),
+        dims=("M", "K", "N"),
+        tg_x=MatmulRowWavesFragment.THREADS,
+        tg_y=1,
+        threadgroup_decls=(lds_decl("B_tile", (2, MatmulRowWavesFragment.TILE_K, MatmulRowWavesFragment.TILE_N)),),
+        helpers=tuple(helpers),
+    )
+    return KernelGroup(
+        kernel=Kernel(fragments=(frag,), ctx=ctx),
+        bindings=(*slots, out_key, *extras.bindings),
+        dims=(M, K, N),
+        grid=(1, M // MatmulRowWavesFragment.TILE_M, 1),
+        threads=(MatmulRowWavesFragment.THREADS, 1, 1),
         ops=decision.ops,
         strategy=decision.strategy,
     )

@@ -17,6 +17,13 @@ from tests import gpu_cases
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _lds_tiled(monkeypatch):
+    """Matmuls 128 columns wide on the LDS-tiled mainloop these tests are
+    about (they take the row-owning-wave kernel by default)."""
+    monkeypatch.setattr(mm, "ROW_WAVES", False)
+
+
 def _divided(M: int, K: int, N: int, plain: bool) -> Operations:
     """Y = (E / s[row]) @ V; with ``plain`` False some rows' divisors (below
     1, zero, subnormal) send their tiles down the per-element k loop."""

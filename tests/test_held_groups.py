@@ -14,6 +14,13 @@ from metellus_amd.runtime import hip_backend
 from tests.gpu_cases import attention_head, mlp_block, plain_matmul
 
 
+@pytest.fixture(autouse=True)
+def _lds_tiled(monkeypatch):
+    """C5 P @ V on the LDS-tiled mainloop these tests are about (it takes the
+    row-owning-wave kernel by default)."""
+    monkeypatch.setattr(mm, "ROW_WAVES", False)
+
+
 def _body(group) -> str:
     return group.kernel.source.split('extern "C"')[-1]
 
