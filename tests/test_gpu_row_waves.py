@@ -100,3 +100,67 @@ def test_attention_heads_batched(monkeypatch):
         v = make()[h].uploads["V"]
         check_matmul(got[True][h].env["O"], e / s1.reshape(-1, 1), v, f"head {h} O", a_rel=2.0 ** -22)
         np.testing.assert_allclose(got[True][h].env["O"], got[False][h].env["O"], rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_row_wave_programs(seed):
+    """Seeded random matmuls the row-owning-wave kernel takes: M of 256 -
+    1024, K of 1024 - 2304, A prologues over one or two row operands (a
+    divisor, plain or not, and a shift) or a scalar, and Lipschitz
+    epilogues -- against the float64 product of the prologue's float32
+    output, at the matmul bar."""
+    rng = np.random.default_rng(7000 + seed)
+    M, K = 256 * int(rng.integers(1, 5)), 128 * int(rng.integers(8, 19))
+    pro = str(rng.choice(["none", "scalar", "divisor", "divisor and shift", "rough divisor"]))
+    epi = str(rng.choice(["none", "relu", "scale"]))
+    r = np.random.default_rng(seed)
+    a = r.standard_normal((M, K)).astype(np.float32)
+    b = (r.standard_normal((K, 128)) / np.sqrt(K)).astype(np.float32)
+    ops = Operations()
+    ops.from_numpy(a, "A")
+    ops.from_numpy(b, "B")
+    ap, cur = a, "A"
+    if pro == "scalar":
+        ops.elementwise("mul", out="P", operands=("A", 1.5))
+        ap, cur = a * np.float32(1.5), "P"
+    elif pro != "none":
+        s = (r.random(M) * 4.0 + 1.0).astype(np.float32)
+        if pro == "rough divisor":
+            s[r.choice(M, 3, replace=False)] = np.array([0.25, 1e-3, 3e-39], dtype=np.float32)
+        ops.from_numpy(s, "s")
+        ops.reshape("s", (M, 1), out="sv")
+        if pro == "divisor and shift":
+            t = r.standard_normal(M).astype(np.float32)
+            ops.from_numpy(t, "t")
+            ops.reshape("t", (M, 1), out="tv")
+            ops.elementwise("subtract", out="Q", operands=("A", "tv"), y_broadcast="col")
+            ops.elementwise("div", out="P", operands=("Q", "sv"), y_broadcast="col")
+            ap = (a - t[:, None]) / s[:, None]
+        else:
+            ops.elementwise("div", out="P", operands=("A", "sv"), y_broadcast="col")
+            with np.errstate(over="ignore"):
+                ap = a / s[:, None]
+        cur = "P"
+    ops.matmul(a=cur, b="B", out="Y")
+    out = "Y"
+    if epi == "relu":
+        ops.elementwise("max", out="Z", operands=("Y", 0.0))
+        out = "Z"
+    elif epi == "scale":
+        ops.elementwise("mul", out="Z", operands=("Y", -0.5))
+        out = "Z"
+    print(f"random row waves {seed}: {(M, K)} prologue {pro} epilogue {epi}", flush=True)
+    res = run(ops, outputs=(out,))
+    assert "mt_rw_chunk(" in res.groups[-1].kernel.source.split('extern "C"')[-1]
+    got = res.env[out].astype(np.float64)
+    # a row whose prologue overflowed (a subnormal divisor) is non-finite
+    # throughout before the epilogue (relu may map its NaNs to 0); its inf /
+    # nan pattern depends on the summation order
+    fin = np.isfinite(ap).all(axis=1)
+    if epi != "relu":
+        assert not np.isfinite(got[~fin]).any()
+    a64, b64 = ap[fin].astype(np.float64), b.astype(np.float64)
+    y = a64 @ b64
+    ref = {"none": y, "relu": np.maximum(y, 0.0), "scale": -0.5 * y}[epi]
+    bound = (1e-4 * np.sqrt(K) + 4e-7) * (np.abs(a64) @ np.abs(b64)) * (0.5 if epi == "scale" else 1.0) + 1e-30
+    assert np.all(np.abs(got[fin] - ref) <= bound), float(np.max(np.abs(got[fin] - ref) / bound))
