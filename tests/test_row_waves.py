@@ -18,7 +18,7 @@ def _body(g) -> str:
     return g.kernel.source.split('extern "C"')[-1]
 
 
-def _program(M=512, K=1024, N=128, prologue="none", epilogue=False, a_view=False) -> Operations:
+def _program(M=512, K=1024, N=128, prologue="none", epilogue=False, a_view=False, b_view=False) -> Operations:
     rng = np.random.default_rng(5)
     ops = Operations()
     if a_view:
@@ -26,7 +26,11 @@ def _program(M=512, K=1024, N=128, prologue="none", epilogue=False, a_view=False
         ops.transpose("As", out="A")
     else:
         ops.from_numpy(rng.standard_normal((M, K)).astype(np.float32), "A")
-    ops.from_numpy(rng.standard_normal((K, N)).astype(np.float32), "B")
+    if b_view:  # B as a transposed view (K^T-like): read along its columns
+        ops.from_numpy(rng.standard_normal((N, K)).astype(np.float32), "Bs")
+        ops.transpose("Bs", out="B")
+    else:
+        ops.from_numpy(rng.standard_normal((K, N)).astype(np.float32), "B")
     a = "A"
     if prologue == "row divisor":
         ops.from_numpy((rng.random(M) + 1.0).astype(np.float32), "s")
@@ -77,7 +81,8 @@ def test_forms_compile(prologue, epilogue):
 @pytest.mark.parametrize(
     "case",
     [
-        dict(N=256), dict(M=300), dict(K=512), dict(K=1088), dict(a_view=True), dict(prologue="column scale"),
+        dict(N=256), dict(M=300), dict(K=512), dict(K=1088), dict(a_view=True), dict(b_view=True),
+        dict(prologue="column scale"),
     ],
 )
 def test_shapes_that_keep_the_lds_tiled_kernel(case):
