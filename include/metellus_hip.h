@@ -61,6 +61,14 @@ int mt_trim(void);
 /* Bytes and blocks in the device block cache (either pointer may be NULL). */
 int mt_cache_info(size_t* cached_bytes, size_t* cached_blocks);
 
+/* No counterpart in the reference.  How many device blocks (hipMallocAsync)
+ * and page-locked host blocks (hipHostMalloc) the shim has requested from
+ * the runtime since the process started, how many buffers its registry holds
+ * (the workspace included), and the workspace's size (0: none yet).  Any
+ * pointer may be NULL.  Lets a caller check that a call allocated nothing. */
+int mt_alloc_stats(uint64_t* device_allocs, uint64_t* host_allocs, uint64_t* live_buffers,
+                   size_t* workspace_bytes);
+
 /* buffer_size (reference: src/metal_backend.mm:105-108). */
 int mt_size(uint64_t handle, size_t* nbytes);
 

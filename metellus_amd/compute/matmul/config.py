@@ -208,10 +208,11 @@ STREAM_K = True
 STREAM_K_MAX_WORKGROUPS = 1023
 
 
-def resident_workgroups(t: TileConfig, anchors: int = 1) -> int:
+def resident_workgroups(t: TileConfig, anchors: int = 1, extra_lds: int = 0) -> int:
     """Workgroups of tile ``t`` one compute unit holds at once, from the LDS
-    size and the register estimate (4 SIMDs x 512 registers per lane)."""
-    by_lds = LDS_BYTES // tile_lds_bytes(t, anchors)
+    size (operand tiles plus ``extra_lds`` bytes the kernel declares beside
+    them) and the register estimate (4 SIMDs x 512 registers per lane)."""
+    by_lds = LDS_BYTES // (tile_lds_bytes(t, anchors) + extra_lds)
     by_vgpr = (4 * (VGPRS_PER_LANE // estimated_vgprs(t, anchors))) // (t.sg_M * t.sg_N)
     return max(1, min(by_lds, by_vgpr))
 

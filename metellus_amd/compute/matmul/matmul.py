@@ -509,9 +509,12 @@ class MatmulMainloopFragment:
         if plain_lds:
             # the tile's divisors are known after its first chunk: one test,
             # then a k loop whose commits carry no per-element branch (or the
-            # same loop with the full chain)
+            # same loop with the full chain).  all_plain is a per-wave ballot;
+            # both loops hold barriers, so the choice is made workgroup-wide
+            # (__syncthreads_and) and every wave enters the same loop.
             body += [
-                "const bool mt_plain = " + " && ".join(ld.render_plain_test() for ld in plain_lds) + ";",
+                "const bool mt_plain = __syncthreads_and(("
+                + " && ".join(ld.render_plain_test() for ld in plain_lds) + ") ? 1 : 0) != 0;",
                 "if (mt_plain) {",
                 *[f"    {x}" for x in loop(True)],
                 "} else {",

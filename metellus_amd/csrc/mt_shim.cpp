@@ -97,6 +97,10 @@ struct State {
     std::multimap<size_t, void*> dev_free;
     size_t dev_cached = 0;
     size_t dev_cache_limit = 0;
+    // Allocations the shim asked the runtime for: device blocks
+    // (hipMallocAsync) and page-locked host blocks (hipHostMalloc).
+    uint64_t device_allocs = 0;
+    uint64_t host_allocs = 0;
     // Workspace of stream-K kernels (a registry buffer the shim owns).
     uint64_t ws_handle = 0;
     size_t ws_bytes = 0;
@@ -150,7 +154,21 @@ constexpr size_t kHostCacheLimit = size_t(1) << 30;   // at most 1 GiB of return
 // block's next owner touches it.
 constexpr size_t kDevGranule = size_t(2) << 20;       // blocks >= 2 MiB: multiples of 2 MiB
 constexpr size_t kDevSmallGranule = 256;               // smaller blocks: multiples of 256 B
-constexpr size_t kDevCacheMax = size_t(64) << 30;      // at most 64 GiB (or a quarter of the device) kept
+// At most 8 GiB (or a sixteenth of the device) of freed blocks are kept by
+// default: several times the working set of the largest program here (C4,
+// ~1.3 GB), little enough that another allocator in the process or another
+// process on the GPU is not starved.  MT_DEVICE_CACHE_MB overrides it (0:
+// every free goes back to the driver); mt_trim empties the cache.
+constexpr size_t kDevCacheMax = size_t(8) << 30;
+
+size_t dev_cache_limit(size_t total_mem) {
+    if (const char* env = std::getenv("MT_DEVICE_CACHE_MB")) {
+        char* end = nullptr;
+        const unsigned long long mb = std::strtoull(env, &end, 10);
+        if (end != env && *end == '\0') return static_cast<size_t>(mb) << 20;
+    }
+    return std::min(kDevCacheMax, total_mem / 16);
+}
 
 size_t dev_capacity(size_t nbytes) {
     const size_t g = nbytes >= kDevGranule ? kDevGranule : kDevSmallGranule;
@@ -265,6 +283,7 @@ int ensure_staging(State& s) {
     hipError_t e = hipSuccess;
     for (int b = 0; b < kStages && e == hipSuccess; ++b) {
         e = hipHostMalloc(&buf[b], kStageChunk, hipHostMallocDefault);
+        if (e == hipSuccess) ++s.host_allocs;
         if (e == hipSuccess) e = hipEventCreateWithFlags(&ev[b], hipEventDisableTiming);
     }
     if (e != hipSuccess) {
@@ -330,7 +349,7 @@ int init_locked(State& s) {
     s.arch = prop.gcnArchName;
     s.cu_count = prop.multiProcessorCount;
     s.clock_khz = prop.clockRate;
-    s.dev_cache_limit = std::min(kDevCacheMax, static_cast<size_t>(prop.totalGlobalMem) / 4);
+    s.dev_cache_limit = dev_cache_limit(static_cast<size_t>(prop.totalGlobalMem));
     MT_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
     // Timing-only events: without the system-scope release at record time
     // (an L2 write-back of the kernel's dirty lines), the bracket measures
@@ -548,6 +567,7 @@ int mt_alloc(size_t nbytes, uint64_t* handle) {
             e = hipMallocAsync(&p, cap, s.stream);
         }
         if (e != hipSuccess) return fail(std::string("hipMallocAsync: ") + hipGetErrorString(e));
+        ++s.device_allocs;
     }
     uint64_t h = s.next_buffer++;
     s.buffers.emplace(h, Buffer{p, nbytes, got});
@@ -561,6 +581,17 @@ int mt_trim(void) {
     if (!s.ready) return 0;
     if (release_dev_cache(s)) return 1;
     MT_HIP(hipStreamSynchronize(s.stream));
+    return 0;
+}
+
+int mt_alloc_stats(uint64_t* device_allocs, uint64_t* host_allocs, uint64_t* live_buffers,
+                   size_t* workspace_bytes) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (device_allocs) *device_allocs = s.device_allocs;
+    if (host_allocs) *host_allocs = s.host_allocs;
+    if (live_buffers) *live_buffers = s.buffers.size();
+    if (workspace_bytes) *workspace_bytes = s.ws_bytes;
     return 0;
 }
 
@@ -668,6 +699,7 @@ int mt_host_alloc(size_t nbytes, void** ptr) {
     }
     void* p = nullptr;
     MT_HIP(hipHostMalloc(&p, want, hipHostMallocDefault));
+    ++s.host_allocs;
     s.host_cap.emplace(p, want);
     *ptr = p;
     return 0;
@@ -872,6 +904,7 @@ int mt_workspace(size_t nbytes, uint64_t* handle) {
         }
         void* p = nullptr;
         MT_HIP(hipMallocAsync(&p, nbytes, s.stream));
+        ++s.device_allocs;
         MT_HIP(hipMemsetAsync(p, 0, kWsHeadBytes, s.stream));  // flags and error word start at 0
         s.ws_handle = s.next_buffer++;
         s.buffers.emplace(s.ws_handle, Buffer{p, nbytes, nbytes});

@@ -318,7 +318,14 @@ def rr_local(M: int, N: int, tile: TileConfig, batch: int = 1) -> bool:
     not limited to a few workgroups)."""
     if ceil_div(N, tile.tile_N) == 1:
         return True
-    return batch * ceil_div(M, tile.tile_M) >= NUM_CUS * resident_workgroups(tile)
+    return batch * ceil_div(M, tile.tile_M) >= NUM_CUS * rr_resident_workgroups(tile)
+
+
+def rr_resident_workgroups(tile: TileConfig) -> int:
+    """Resident workgroups of a matmul with the row-reduction epilogue: its
+    per-wave-column row array sits in LDS beside the operand tiles."""
+    rows, cols = rr_lds_shape(tile)
+    return resident_workgroups(tile, extra_lds=4 * rows * cols)
 
 
 def assemble_matmul(decision: DecisionView, function_name: str | None, batch: int = 1) -> KernelGroup:
@@ -400,7 +407,7 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
     stream_k = red is None and uses_stream_k(M, K, N, tile, n_persistent, batch)
     local_rr = red is not None and rr_local(M, N, tile, batch)
     if local_rr:
-        n_persistent = min(ceil_div(M, tile.tile_M), max(1, NUM_CUS * resident_workgroups(tile) // batch))
+        n_persistent = min(ceil_div(M, tile.tile_M), max(1, NUM_CUS * rr_resident_workgroups(tile) // batch))
     persistent = PersistentTiles(tile.tile_M, tile.tile_N, stream_k=stream_k, tile_K=tile.tile_K,
                                  row_blocks=local_rr) if n_persistent else None
     spread = load_spread(pro_a, pro_b)

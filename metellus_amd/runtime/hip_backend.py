@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "mt_free",
     "mt_trim",
     "mt_cache_info",
+    "mt_alloc_stats",
     "mt_size",
     "mt_device_ptr",
     "mt_write",
@@ -91,6 +92,10 @@ def _load():
             "mt_free": ([_u64, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
             "mt_trim": ([], ctypes.c_int),
             "mt_cache_info": ([ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+            "mt_alloc_stats": (
+                [ctypes.POINTER(_u64), ctypes.POINTER(_u64), ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_size_t)],
+                ctypes.c_int,
+            ),
             "mt_size": ([_u64, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
             "mt_device_ptr": ([_u64, ctypes.POINTER(_u64)], ctypes.c_int),
             "mt_write": ([_u64, ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int),
@@ -208,6 +213,18 @@ def device_cache_info() -> tuple[int, int]:
     nb, nk = ctypes.c_size_t(0), ctypes.c_size_t(0)
     _check(_load().mt_cache_info(ctypes.byref(nb), ctypes.byref(nk)))
     return nb.value, nk.value
+
+
+def alloc_stats() -> dict:
+    """Allocations the shim has requested from the runtime so far
+    (``device_allocs``: hipMallocAsync, ``host_allocs``: hipHostMalloc), the
+    buffers its registry holds (``live_buffers``, the workspace included) and
+    the workspace's size (``workspace_bytes``, 0 before the first stream-K
+    launch)."""
+    d, h, n = _u64(0), _u64(0), _u64(0)
+    w = ctypes.c_size_t(0)
+    _check(_load().mt_alloc_stats(ctypes.byref(d), ctypes.byref(h), ctypes.byref(n), ctypes.byref(w)))
+    return {"device_allocs": d.value, "host_allocs": h.value, "live_buffers": n.value, "workspace_bytes": w.value}
 
 
 def buffer_size(handle: int) -> int:
@@ -363,11 +380,54 @@ def init() -> None:
     _check(_load().mt_init())
 
 
+def _check_slot(item) -> bool:
+    """Validate one ``run_kernel`` slot; True when it is an array (a one-shot
+    buffer with write-back).  Like the reference (src/metal_backend.mm:153-176):
+    an object with ``.handle`` or an int is a persistent buffer, an ndarray a
+    transient one."""
+    if hasattr(item, "handle") or isinstance(item, (int, np.integer)):
+        return False
+    if not isinstance(item, np.ndarray):
+        raise TypeError(f"run_kernel: a slot is a Buffer, an int handle or an ndarray; got {type(item).__name__}")
+    if not item.flags["C_CONTIGUOUS"] or not item.flags["WRITEABLE"]:
+        # the reference's binding refuses read-only arrays too
+        raise ValueError("run_kernel: an array slot must be C-contiguous and writeable (its contents are written back in place)")
+    return True
+
+
 def run_kernel(source: str, function_name: str, buffers, grid, threads, *, dims=(), dims_slot=None) -> dict:
     """Compile (cached) + launch + wait, returning ``{"time_ms": t}`` like the
-    reference (reference: src/metal_backend.mm:178-249).  ``dims`` are passed
-    by value at ``dims_slot`` (default: after the buffers)."""
+    reference (reference: src/metal_backend.mm:178-249).  ``buffers`` holds
+    one slot per kernel buffer parameter, in order: a Buffer, an int handle,
+    or a NumPy array, which is uploaded to a one-shot device buffer and, once
+    the kernel has finished, copied back into the array (slots in order) --
+    so an output array receives the kernel's result (reference:
+    src/metal_backend.mm:235-239).  Slots are checked before anything is
+    compiled or allocated.  ``dims`` are passed by value at ``dims_slot``
+    (default: after the buffers)."""
+    items = list(buffers)
+    is_array = [_check_slot(item) for item in items]
     k = compile_kernel(source, function_name)
-    slot = len(buffers) if dims_slot is None else int(dims_slot)
-    t = launch(k, buffers, dims, slot, grid, threads, timed=True)
+    handles: list[int] = []
+    transient: list[tuple[int, np.ndarray]] = []
+    try:
+        for item, arr in zip(items, is_array):
+            if not arr:
+                handles.append(_handle_of(item))
+                continue
+            # a zero-size array still binds a valid (unused) pointer
+            h = create_buffer(max(int(item.nbytes), 4))
+            transient.append((h, item))
+            handles.append(h)
+            if item.nbytes:
+                write_buffer(h, item)
+        slot = len(handles) if dims_slot is None else int(dims_slot)
+        # a timed launch waits for the kernel, so the write-backs read its result
+        t = launch(k, handles, dims, slot, grid, threads, timed=True)
+        for h, target in transient:
+            if target.nbytes:
+                read_buffer(h, target)
+    finally:
+        for h, _ in transient:
+            release_buffer(h)
     return {"time_ms": t}

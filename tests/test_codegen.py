@@ -248,3 +248,20 @@ def test_plain_divisors_only_for_gathered_divisors():
     code = ChainCode((div,), ("x",), "p", fast_div=True)
     assert code.plain_predicate_lambda() == "[=](const mt_vals<1>& e) -> bool { return mt_div_plain(e.v[0]); }"
     assert "p_plain(" in code.helpers()[1] and "mt_div_rcp(" in code.helpers()[1]
+
+
+def test_plain_divisor_split_is_workgroup_uniform(monkeypatch):
+    """The LDS-tiled mainloop tests a tile's gathered divisors once and runs
+    one of two k loops, each with a barrier per chunk.  The test is a per-wave
+    ballot, so the choice goes through __syncthreads_and: every wave of the
+    workgroup enters the same loop and meets the same barriers."""
+    from metellus_amd.orchestrator.assembly import matmul as am
+
+    monkeypatch.setattr(am, "ROW_WAVES", False)
+    g = _by_name(compile_program(gpu_cases.attention_head(512, 256)))["matmul_O_fused"]
+    body = g.kernel.source.split('extern "C"')[1]
+    split = [ln.strip() for ln in body.splitlines() if "mt_plain =" in ln]
+    assert split and all(s.startswith("const bool mt_plain = __syncthreads_and((") for s in split)
+    assert all(s.endswith(") ? 1 : 0) != 0;") and "all_plain<" in s for s in split)
+    assert "if (mt_plain) {" in body
+    assert hip_backend.compile_only(g.kernel.source) > 0

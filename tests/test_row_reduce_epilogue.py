@@ -239,3 +239,27 @@ def test_cases_that_do_not_fuse(case, monkeypatch):
     off = _groups(ops, False, monkeypatch)
     assert all(g.strategy is not FusionStrategy.MATMUL_REDUCTION_EPILOGUE for g in on)
     assert [g.strategy for g in on] == [g.strategy for g in off]
+
+
+def test_residency_counts_the_row_array(monkeypatch):
+    """The row-reduction epilogue's LDS row array (``rr_lds_shape``) is part
+    of what limits resident workgroups: the local form's persistent grid and
+    its choice of form count it beside the operand tiles.  With an LDS size
+    that holds two workgroups' operand tiles but not two row arrays as well,
+    one workgroup is resident, and the choice of form follows."""
+    from metellus_amd.compute.matmul import config as cfg
+    from metellus_amd.compute.matmul.matmul import rr_lds_shape
+    from metellus_amd.orchestrator.assembly import matmul as mm
+
+    tile = cfg.select_tile_config(512, 256, 1024)  # 128 x 128 tiles
+    rows, cols = rr_lds_shape(tile)
+    tiles = cfg.tile_lds_bytes(tile)
+    assert cfg.resident_workgroups(tile) == mm.rr_resident_workgroups(tile) == 2  # gfx950's 160 KiB
+    monkeypatch.setattr(cfg, "LDS_BYTES", 2 * tiles + 4 * rows * cols - 4)
+    assert cfg.resident_workgroups(tile) == 2 and mm.rr_resident_workgroups(tile) == 1
+    # 256 row blocks of 128 x 128 tiles fill one round of one resident
+    # workgroup per CU (local form) but not of two
+    assert mm.rr_local(256 * 128, 4 * 128, tile)
+    monkeypatch.setattr(cfg, "LDS_BYTES", 2 * (tiles + 4 * rows * cols))
+    assert mm.rr_resident_workgroups(tile) == 2
+    assert not mm.rr_local(256 * 128, 4 * 128, tile)

@@ -7,9 +7,16 @@ tiles), then smaller forced-capacity matmuls and a diamond with two
 accumulator sets, whose calls reuse the same scratch; and the matmul ->
 reduction epilogue extension in its workspace form (row-block counters in
 the scratch's flag words).  The scratch error word stays 0, and a request
-beyond the scratch's size is refused before anything is launched."""
+beyond the scratch's size is refused before anything is launched.  Around
+every allocation-free call the shim's allocation counters, its live buffers
+and its workspace size stay as they were; in a fresh process the call runs
+before any workspace exists and leaves none behind."""
 
 from __future__ import annotations
+
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -43,7 +50,7 @@ def _both(ops, out_name: str):
         bufs = [inputs[k] if k in inputs else out for k in g.bindings]
         args = (g.kernel.handle, bufs, g.dims, g.kernel.dims_slot_index, g.grid, g.threads)
         if noalloc:
-            assert hip_backend.launch_noalloc(*args, scratch=ws) == 0
+            _noalloc_call(args, ws)
         else:
             hip_backend.launch(*args, workspace=ws)
             hip_backend.check_workspace()
@@ -52,6 +59,15 @@ def _both(ops, out_name: str):
     for b in inputs.values():
         b.release()
     return outs
+
+
+def _noalloc_call(args, ws: int) -> None:
+    """One mt_launch_noalloc call (waited for) that must allocate nothing:
+    the shim's device and host allocation counts, its live buffers and its
+    workspace size are the same before and after it."""
+    before = hip_backend.alloc_stats()
+    assert hip_backend.launch_noalloc(*args, scratch=ws) == 0
+    assert hip_backend.alloc_stats() == before
 
 
 def _forced(monkeypatch, capacity):
@@ -135,7 +151,7 @@ def test_noalloc_runs_the_row_reduction_epilogue(monkeypatch):
             bufs = [inputs[k] if k in inputs else outs[k] for k in g.bindings]
             args = (g.kernel.handle, bufs, g.dims, g.kernel.dims_slot_index, g.grid, g.threads)
             if noalloc:
-                assert hip_backend.launch_noalloc(*args, scratch=ws) == 0
+                _noalloc_call(args, ws)
             else:
                 hip_backend.launch(*args, workspace=ws)
                 hip_backend.check_workspace()
@@ -149,3 +165,45 @@ def test_noalloc_runs_the_row_reduction_epilogue(monkeypatch):
         for k in a:
             np.testing.assert_array_equal(a[k], b[k])
         np.testing.assert_array_equal(a["r"], a["Yc"].max(axis=1))
+
+
+def fresh_process_check() -> None:
+    """Run in a process of its own: an allocation-free call before any
+    mt_launch has created the shim's workspace allocates nothing and creates
+    no workspace; its output then matches mt_launch's bit for bit."""
+    config.PERSISTENT, config.PERSISTENT_CAPACITY, config.STREAM_K = True, 5, True
+    hip_backend.init()
+    assert hip_backend.alloc_stats()["workspace_bytes"] == 0
+    ops = gpu_cases.plain_matmul(1024, 256, 1024, seed=34)
+    (g,) = compile_program(ops)
+    ws = g.kernel.workspace_bytes
+    assert ws > 0
+    inputs = {k: Buffer.from_numpy(a) for k, a in ops.uploads.items()}
+    outs = []
+    for noalloc in (True, False):
+        out = Buffer(1024 * 1024 * 4)
+        out.fill(0xFF)
+        bufs = [inputs[k] if k in inputs else out for k in g.bindings]
+        args = (g.kernel.handle, bufs, g.dims, g.kernel.dims_slot_index, g.grid, g.threads)
+        if noalloc:
+            _noalloc_call(args, ws)
+            assert hip_backend.alloc_stats()["workspace_bytes"] == 0
+        else:
+            hip_backend.launch(*args, workspace=ws)
+            hip_backend.check_workspace()
+            assert hip_backend.alloc_stats()["workspace_bytes"] >= ws
+        outs.append(out.numpy((1024, 1024), np.float32))
+    assert not np.isnan(outs[0]).any()
+    np.testing.assert_array_equal(outs[0], outs[1])
+    print("fresh-process no-alloc check: ok", flush=True)
+
+
+def test_noalloc_first_call_in_a_fresh_process():
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("noalloc: fresh process, no workspace yet", flush=True)
+    r = subprocess.run(
+        [sys.executable, "-c", "from tests.test_zz_no_alloc import fresh_process_check; fresh_process_check()"],
+        cwd=root, capture_output=True, text=True, timeout=110,
+    )
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "fresh-process no-alloc check: ok" in r.stdout
