@@ -736,6 +736,195 @@ class MatmulRowWavesFragment:
         return (TgmemAccess("B_tile", "read", 2 * 64 * 128, (2, 64, 128)),)
 
 
+# K-resident row waves: the previous chunk's right half is stored one row
+# after every KR_STORE_STRIDE-th MFMA group of this chunk's left half (1:
+# after each of the first four groups); this chunk's left half one row after
+# each of the first four groups of its right half.  KR_STORE_POLICY is the
+# buffer stores' cache-policy operand (0: default; 16: sc1, device scope,
+# written through the L2).  Measured on C5 S (32 heads, medians of 25-30
+# launches, one box):
+# stores after the chunk's MFMAs 263.4 us; one row per group of the other
+# half 255.1; spread over every other group of the left half 251.2; sc1
+# 246.7; the right half's stores in the first four groups 245.6 (0.889 of
+# the fp32 MFMA peak).  Without any stores: 239.7.  Per chunk 14.8 us
+# against 13.6 of MFMA work, plus ~13 us fixed (launch, first loads, last
+# stores).  The first chunk waits for all of A as well as its B: a partial
+# vmcnt counting only the A loads issued after the B chunk is not a safe
+# wait for that chunk (direct-to-LDS loads and ordinary loads do not
+# retire in issue order), and it gained under 1 us.
+KR_STORE_STRIDE = 2
+KR_STORE_POLICY = 16
+
+
+@dataclass(frozen=True)
+class MatmulKResidentFragment:
+    """A matmul with a short K (64 or 128) and an n-major B (read along K,
+    such as the transposed view K^T) on K-resident row waves (``mt_kr_*``):
+    1024 lanes own 256 rows, each wave 16 of them, whose whole K sits in its
+    registers (loaded once; the prologue applied there).  The workgroup walks
+    ``chunks`` 128-column chunks of B, staged by direct-to-LDS loads in two
+    LDS stages ``B_tile[2][128][K]``; every chunk is a finished 256 x 128
+    output tile on 16x16x4 MFMAs, walked column half by column half.  Its
+    stores (128 bits per row) go out between MFMAs: one row of the
+    previous chunk's right half after each of the first 4 MFMA groups of
+    this chunk's left half, one row of this chunk's left half after each of
+    the first 4 groups of its right half (the halves use disjoint
+    accumulators, so no register holds a result longer).  Workgroup (x, y) takes rows
+    256 y .. 256 y + 255 and columns 128 chunks x onwards.  ``prologue``:
+    None, ``("transform", lambda)`` over (raw, row, col), or
+    ``("gather", gather, apply)`` with operands fixed per row.
+    ``value_expr``: a format string over ``{a0}`` with ``row`` and ``col`` in
+    scope.  Needs M % 256 == 0, N % (128 chunks) == 0 and an output (one
+    program's) below 2 GiB: stores address it by 32-bit byte offsets.
+
+    ``reduction`` = (op, red_name): the kernel also reduces every output row
+    (after the epilogue) into ``red_name[row]``; the workgroup then walks
+    whole rows (one column group).  Each lane folds its values of each of
+    its 4 rows in column order (chunk, then column half, then column), and
+    the 16 lanes sharing a row combine by xor-butterfly over lane bits 0..3,
+    low bit first -- one fixed order, the same for every batch size."""
+
+    a_name: str
+    b_name: str
+    c_name: str
+    a_row_stride: int
+    b_col_stride: int
+    K: int
+    chunks: int
+    prologue: tuple | None = None
+    value_expr: str | None = None
+    reduction: tuple[str, str] | None = None
+    name: str = "matmul_k_resident"
+    kind: str = "compute"
+
+    TILE_M = 256
+    TILE_N = 128
+    THREADS = 1024
+
+    def _prologue_lines(self) -> list[str]:
+        pro, K = self.prologue, self.K
+        if pro is None:
+            return []
+        if pro[0] == "transform":
+            lines = [f"const auto xt = {pro[1]};"]
+            apply = "xt(mt_a[q][e], mt_row, mt_k0 + 4u * (unsigned)q + (unsigned)e)"
+        else:
+            _, gather, app = pro[:3]
+            lines = [f"const auto xg = {gather};", f"const auto xa = {app};",
+                     "const auto mt_e = xg(mt_row, 0u);  // the row's operands"]
+            apply = "xa(mt_a[q][e], mt_e)"
+        return lines + [
+            f"const unsigned mt_k0 = {K // 4}u * (lane >> 4);",
+            "(void)mt_k0;",
+            "#pragma unroll",
+            f"for (int q = 0; q < {K // 16}; ++q)",
+            "#pragma unroll",
+            f"    for (int e = 0; e < 4; ++e) mt_a[q][e] = {apply};",
+        ]
+
+    def render(self, ctx: CodegenContext) -> str:
+        a, b, c, K = self.a_name, self.b_name, self.c_name, self.K
+        if K not in (64, 128):
+            raise ValueError(f"K-resident rows hold K = 64 or 128; got {K}")
+        bcs = self.b_col_stride
+        value = self.value_expr.format(a0="acc[4 * h + j][i]") if self.value_expr else "acc[4 * h + j][i]"
+        red = self.reduction
+        opc, ident = _RR_OPS[red[0]] if red is not None else (None, None)
+        T = K // 16
+        # the previous right half: one row every st groups of the left half
+        st = max(1, min(KR_STORE_STRIDE, T // 4))
+        lines = [
+            "const unsigned lane = mt_lane();",
+            "const unsigned wave = mt_wave();",
+            "const unsigned tile_m0 = blockIdx.y * 256u;",
+            f"const unsigned mt_n0 = blockIdx.x * {128 * self.chunks}u;",
+            "const unsigned mt_row = tile_m0 + wave * 16u + (lane & 15u);",
+            f"const mt_kr_dma<{K}, 1024> ld_B({bcs}u, threadIdx.x);",
+            f"ld_B.fetch({b}, {bcs}u, mt_n0, &B_tile[0][0][0]);",
+            f"const float* __restrict__ mt_arow = {a} + (size_t)mt_row * {self.a_row_stride}u + {K // 4}u * (lane >> 4);",
+            f"mt_f32x4 mt_a[{T}];",
+            "#pragma unroll",
+            f"for (int q = 0; q < {T}; ++q) mt_a[q] = mt_ld4(mt_arow + 4u * (unsigned)q);",
+            *self._prologue_lines(),
+            "mt_f32x4 acc[8];",
+            "#pragma unroll",
+            "for (int j = 0; j < 8; ++j) acc[j] = mt_f32x4{0.f, 0.f, 0.f, 0.f};",
+            *([f"float mt_red[4] = {{{ident}, {ident}, {ident}, {ident}}};"] if red is not None else []),
+            "// row i of a finished column half h (blocks 4h .. 4h + 3) of the chunk",
+            "// at columns col_base: the epilogue, then one 128-bit buffer store at",
+            "// this lane's byte offset plus a wave-uniform one",
+            f"const mt_u32x4 mt_rs = mt_raw_buffer({c});",
+            "const unsigned mt_voff = ((tile_m0 + wave * 16u + 4u * (lane >> 4)) * N + mt_n0 + 4u * (lane & 15u)) * 4u;",
+            "const auto mt_store_row = [&](int h, int i, unsigned col_base) {",
+            "    const unsigned row = tile_m0 + wave * 16u + 4u * (lane >> 4) + (unsigned)i;",
+            "    const unsigned col0 = col_base + 64u * (unsigned)h + 4u * (lane & 15u);",
+            "    mt_f32x4 mt_o;",
+            "#pragma unroll",
+            "    for (int j = 0; j < 4; ++j) {",
+            "        const unsigned col = col0 + (unsigned)j;",
+            "        (void)col;",
+            f"        mt_o[j] = {value};",
+            *([f"        mt_red[i] = mt_rr_op<{opc}>(mt_red[i], mt_o[j]);"] if red is not None else []),
+            "    }",
+            f"    mt_buffer_store4<{KR_STORE_POLICY}>(mt_o, mt_rs, mt_voff, "
+            "((unsigned)i * N + (col_base - mt_n0) + 64u * (unsigned)h) * 4u);",
+            "};",
+            "__builtin_amdgcn_s_waitcnt(0);",
+            "__syncthreads();",
+            f"for (unsigned ch = 0; ch < {self.chunks}u; ++ch) {{",
+            f"    if (ch + 1u < {self.chunks}u) ld_B.fetch({b}, {bcs}u, mt_n0 + (ch + 1u) * 128u, "
+            "&B_tile[(ch + 1u) & 1u][0][0]);",
+            "    const unsigned col_base = mt_n0 + ch * 128u;",
+            "    // while the left half's MFMAs run: the previous chunk's right half,",
+            "    // one row per group; while the right half's run: this chunk's left",
+            "    const auto mt_hook = [&](int q) {",
+            f"        if (q < {4 * st} && q % {st} == 0) {{",
+            f"            if (ch > 0u) mt_store_row(1, q / {st}, col_base - 128u);",
+            f"            if (q == {3 * st}) {{",
+            "#pragma unroll",
+            "                for (int j = 4; j < 8; ++j) acc[j] = mt_f32x4{0.f, 0.f, 0.f, 0.f};",
+            "            }",
+            f"        }} else if (q >= {T} && q < {T + 4}) {{",
+            f"            mt_store_row(0, q - {T}, col_base);",
+            f"            if (q == {T + 3}) {{",
+            "#pragma unroll",
+            "                for (int j = 0; j < 4; ++j) acc[j] = mt_f32x4{0.f, 0.f, 0.f, 0.f};",
+            "            }",
+            "        }",
+            "    };",
+            f"    mt_kr_chunk<{K}>(mt_a, &B_tile[ch & 1u][0][0], lane, acc, mt_hook);",
+            "    // the next chunk's B has landed (and the stores issued a half",
+            "    // chunk ago have drained)",
+            "    __builtin_amdgcn_s_waitcnt(0);",
+            "    __syncthreads();",
+            "}",
+            "// the last chunk's right half",
+            "#pragma unroll",
+            f"for (int i = 0; i < 4; ++i) mt_store_row(1, i, mt_n0 + {128 * (self.chunks - 1)}u);",
+        ]
+        if red is not None:
+            lines += [
+                "// the 16 lanes holding a row: xor-butterfly over lane bits 0..3",
+                "#pragma unroll",
+                "for (int i = 0; i < 4; ++i) {",
+                f"    mt_red[i] = mt_rr_op<{opc}>(mt_red[i], mt_xor_lanes<1u>(mt_red[i]));",
+                f"    mt_red[i] = mt_rr_op<{opc}>(mt_red[i], mt_xor_lanes<2u>(mt_red[i]));",
+                f"    mt_red[i] = mt_rr_op<{opc}>(mt_red[i], mt_xor_lanes<4u>(mt_red[i]));",
+                f"    mt_red[i] = mt_rr_op<{opc}>(mt_red[i], mt_xor_lanes<8u>(mt_red[i]));",
+                "}",
+                "if ((lane & 15u) == 0u) {",
+                "    const unsigned row0 = tile_m0 + wave * 16u + 4u * (lane >> 4);",
+                "#pragma unroll",
+                f"    for (int i = 0; i < 4; ++i) {red[1]}[row0 + (unsigned)i] = mt_red[i];",
+                "}",
+            ]
+        return "{\n" + textwrap.indent("\n".join(lines), "    ") + "\n}"
+
+    @property
+    def tgmem_accesses(self) -> tuple[TgmemAccess, ...]:
+        return (TgmemAccess("B_tile", "read", 2 * 128 * self.K, (2, 128, self.K)),)
+
+
 def _nonempty(lines) -> list[str]:
     return [x for x in lines if x]
 

@@ -69,9 +69,11 @@ MT_INLINE mt_f32x4 mt_ld4_nt(const float* p) {
 MT_INLINE void mt_st4_nt(float* p, mt_f32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<mt_f32x4*>(p)); }
 // 128-bit global store at device scope (sc1): it writes through the XCD's L2
 // instead of leaving a dirty line there, which suits outputs written once by
-// streaming kernels.  p must point to global memory (never LDS).
+// streaming kernels.  p must point to global memory (never LDS).  A 128-bit
+// store reads its data registers after it issues; the compiler cannot see
+// this store, so it is followed by two wait states (see mt_buffer_store4).
 MT_INLINE void mt_st4_wt(float* p, mt_f32x4 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
 }
 
 // x / y where the quotient enters a matmul.  r is the hardware reciprocal
@@ -998,6 +1000,179 @@ MT_INLINE void mt_rw_chunk(const mt_f32x4 (&a)[4], const float* __restrict__ Bs,
 MT_INLINE void mt_rw_load(mt_f32x4 (&a)[4], const float* __restrict__ arow, unsigned k0) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) a[q] = mt_ld4(arow + k0 + 4u * (unsigned)q);
+}
+
+// ---------------------------------------------------------------------------
+// K-resident row waves for matmuls with a short K (64 or 128) whose B is read
+// along K (n-major: B[k][n] at n * ldb + k, such as the transposed view K^T
+// of attention scores).  Each of a workgroup's 16 waves owns 16 rows of a
+// 256-row block and keeps those rows' whole K in registers (K/4 floats per
+// lane, loaded once).  B streams through LDS in 128-column chunks, n-major
+// [128][K], two stages; each chunk is a finished 256 x 128 output tile, 8
+// column blocks of v_mfma_f32_16x16x4f32 per wave, stored with 128-bit
+// stores issued between the MFMAs of the next column half.
+//   k: lane group g = l/16 takes k = g K/4 + s at step s < K/4, so its A
+//      values are K/4 consecutive floats of its row (128-bit loads), and its
+//      B values of 4 consecutive steps are one 128-bit LDS read, logical
+//      16-byte slot g K/16 + t (t = s/4) of the B row;
+//   n: column block j puts lane column c = l%16 at output column
+//      64 (j/4) + 4c + j%4, so blocks 4h .. 4h + 3 give a lane 4 consecutive
+//      output columns of each of its rows (a 128-bit store; 256 contiguous
+//      bytes per 16 lanes);
+//   LDS: B row n (K/4 slots) holds logical slot L at physical slot
+//      L ^ mt_kr_swz(n).  gfx950 serves a ds_read_b128 in 4 passes of 16
+//      lanes, each pass two 8-lane groups k and k ^ 3 of one half-wave
+//      (lanes 0-7 with 24-31, 8-15 with 16-23, ...), from 64 4-byte banks
+//      (byte address mod 256) -- measured with rocprof's LDS bank-conflict
+//      counter on fixed lane/address patterns.  Lane (g, c) reads row
+//      64 (j/4) + 4c + j%4 at logical slot g K/16 + t, and a pass holds
+//      lanes c < 8 of one g with lanes c >= 8 of g ^ 1.  So mt_kr_swz(n) is
+//      c mod 8 for K = 128 (bit 3 of the slot then follows g) and c for
+//      K = 64 (bit 3 follows c): the 16 lanes of every pass hit 16
+//      distinct 16-byte bank groups.
+// ---------------------------------------------------------------------------
+
+template <int K>
+MT_HD unsigned mt_kr_swz(unsigned n) {
+    static_assert(K == 64 || K == 128, "K-resident rows hold K = 64 or 128");
+    return (n >> 2) & (K == 128 ? 7u : 15u);
+}
+
+// Where wave-load `inst`, lane `lane` of the B loader puts its 16 bytes: row r
+// of the [128][K] chunk, physical slot p = (64 inst + lane) mod K/4; it loads
+// the row's logical slot p ^ mt_kr_swz(r).
+template <int K>
+MT_HD void mt_kr_slot(unsigned inst, unsigned lane, unsigned& r, unsigned& logical) {
+    constexpr unsigned S = K / 4;
+    const unsigned slot = inst * 64u + lane;
+    r = slot / S;
+    logical = (slot % S) ^ mt_kr_swz<K>(r);
+}
+
+// 128 n-major B rows of K floats (row stride ldb floats, a multiple of 4)
+// into a dense swizzled LDS chunk [128][K] by direct-to-LDS loads; each
+// lane's byte offsets from the chunk origin are computed once.
+template <int K, int NT>
+struct mt_kr_dma {
+    static constexpr int S = K / 4;
+    static constexpr int INSTR = 128 * S / 64;
+    static constexpr int PERW = INSTR / (NT / 64);
+    static_assert(INSTR % (NT / 64) == 0, "the chunk must split into the same number of wave loads per wave");
+    unsigned off[PERW];
+    unsigned lds_off;
+
+    MT_INLINE mt_kr_dma(unsigned ldb, unsigned tid) {
+        const unsigned lane = tid & 63u;
+        const unsigned wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        lds_off = wave * PERW * 1024u;
+#pragma unroll
+        for (int q = 0; q < PERW; ++q) {
+            unsigned r, logical;
+            mt_kr_slot<K>(wave * PERW + q, lane, r, logical);
+            off[q] = (r * ldb + 4u * logical) * 4u;
+        }
+    }
+
+    // B rows n0 .. n0 + 127 of src (B[k][n] = src[n * ldb + k]).
+    MT_INLINE void fetch(const float* __restrict__ src, unsigned ldb, unsigned n0, float* lds) const {
+        const unsigned long long origin = mt_uniform_addr(src + (size_t)n0 * ldb);
+        const unsigned base = __builtin_amdgcn_readfirstlane(mt_lds_addr(lds)) + lds_off;
+#pragma unroll
+        for (int q = 0; q < PERW; ++q) mt_dma16(origin, off[q], base + (unsigned)q * 1024u);
+    }
+};
+
+// The B values of one group: quad t (4 steps), column half h (blocks
+// 4h .. 4h + 3): rows 64h + 4c + jj of the chunk, logical slot g K/16 + t.
+struct mt_kr_group {
+    mt_f32x4 b[4];
+};
+
+template <int K>
+MT_INLINE mt_f32x4 mt_kr_b(const float* __restrict__ bl, unsigned phys_slot, int h, int jj) {
+    return mt_ld4(bl + (unsigned)(64 * h + jj) * K + 4u * phys_slot);
+}
+
+struct mt_kr_no_hook {
+    MT_INLINE void operator()(int) const {}
+};
+
+// One 128-column chunk from the B stage at Bs and this lane's K/4 A values
+// (already transformed by any prologue), column half by column half: groups
+// q = 0 .. K/8 - 1 are quad t = q mod K/16 of half h = q / (K/16), 16 MFMAs
+// each, steps 0 .. 3 in turn over the half's 4 blocks.  The group's B
+// values sit in one set of 16 registers: block jj's value for the next
+// group is read right after its step-3 MFMA (the order pinned with
+// sched_barrier; measured on C5 S, as fast as two register sets, which
+// cost 15 more VGPRs).  hook(q) runs after
+// group q's MFMAs are issued -- the kernel stores one row of the other
+// half's finished accumulators there, so the stores go out between MFMAs.
+// The k order per output element is fixed: quads t = 0 .. K/16 - 1, steps
+// 0 .. 3 within each.
+template <int K, typename H = mt_kr_no_hook>
+MT_INLINE void mt_kr_chunk(const mt_f32x4 (&a)[K / 16], const float* __restrict__ Bs, unsigned lane,
+                           mt_f32x4 (&acc)[8], H hook = H{}) {
+    constexpr int T = K / 16;
+    const unsigned c = lane & 15u;
+    const unsigned g = lane >> 4;
+    const float* __restrict__ bl = Bs + 4u * c * (unsigned)K;
+    const unsigned sw = mt_kr_swz<K>(4u * c);  // the same for every row this lane reads
+    __builtin_amdgcn_s_setprio(1);
+    mt_kr_group f;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) f.b[jj] = mt_kr_b<K>(bl, (g * (unsigned)T) ^ sw, 0, jj);
+#pragma unroll
+    for (int q = 0; q < 2 * T; ++q) {
+        const int h = q / T, t = q % T;
+        const int hn = (q + 1) / T, tn = (q + 1) % T;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ss = 0; ss < 3; ++ss)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                acc[4 * h + jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][ss], f.b[jj][ss], acc[4 * h + jj], 0, 0, 0);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            acc[4 * h + jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][3], f.b[jj][3], acc[4 * h + jj], 0, 0, 0);
+            if (q + 1 < 2 * T) f.b[jj] = mt_kr_b<K>(bl, (g * (unsigned)T + (unsigned)tn) ^ sw, hn, jj);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        hook(q);
+    }
+    __builtin_amdgcn_s_setprio(0);
+}
+
+// Raw buffer access to an output: one descriptor per workgroup (32-bit data,
+// stride 0, the whole 4 GiB range), so a store takes one per-lane byte
+// offset and one wave-uniform one instead of a 64-bit address per lane.
+typedef unsigned mt_u32x4 __attribute__((ext_vector_type(4)));
+
+MT_INLINE mt_u32x4 mt_raw_buffer(const void* p) {
+    const unsigned long long a = mt_uniform_addr(static_cast<const float*>(p));
+    return mt_u32x4{(unsigned)a, (unsigned)(a >> 32) & 0xffffu, 0xffffffffu, 0x00020000u};
+}
+
+// 16 bytes to rs + voff + soff (POLICY 16: sc1, device scope, written
+// through the L2; 0: default).  The store reads its data registers after
+// it issues, so nothing may write them in the next cycles: on MI355X a
+// v_mul writing the first data register right after a 128-bit buffer store
+// (the compiler inserts no wait state for a buffer store with an SGPR
+// soffset) let the store write the new value in lanes 12-15 of a 16-lane
+// group -- the next row's score in C5 S, in 16-32 elements per run.  The
+// store is therefore issued here with two wait states behind it.
+template <int POLICY = 0>
+MT_INLINE void mt_buffer_store4(mt_f32x4 v, mt_u32x4 rs, unsigned voff, unsigned soff) {
+    const unsigned so = __builtin_amdgcn_readfirstlane(soff);
+    if constexpr (POLICY == 16)
+        asm volatile("buffer_store_dwordx4 %0, %1, %2, %3 offen sc1\n\ts_nop 1"
+                     :
+                     : "v"(v), "v"(voff), "s"(rs), "s"(so)
+                     : "memory");
+    else
+        asm volatile("buffer_store_dwordx4 %0, %1, %2, %3 offen\n\ts_nop 1"
+                     :
+                     : "v"(v), "v"(voff), "s"(rs), "s"(so)
+                     : "memory");
 }
 
 // Row (within a 32x32 output block) of accumulator register v held by `lane`;

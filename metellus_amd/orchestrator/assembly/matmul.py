@@ -39,6 +39,7 @@ from metellus_amd.compute.matmul.matmul import (
     MatmulComputeFragment,
     MatmulConfig,
     MatmulEpilogueStoreFragment,
+    MatmulKResidentFragment,
     MatmulMainloopFragment,
     MatmulRowReduceFinishFragment,
     MatmulRowReduceSetupFragment,
@@ -282,6 +283,59 @@ def row_waves(M: int, K: int, N: int, src_a: Tensor, src_b: Tensor, pro_a: Chain
     return pro_a is None or pro_a.external_axes() <= {"row"}
 
 
+# K-resident row waves (MatmulKResidentFragment): a matmul with K = 64 or
+# 128 and an n-major B (attention's S = Q @ K^T reads K^T along K) keeps each
+# wave's 16 rows of A for the whole K in registers and streams B through LDS
+# in 128-column chunks; each chunk is a whole output tile, so no tile drains
+# and the output stores of one chunk drain during the next chunk's MFMAs.
+# The LDS-tiled kernel walks 256 x 256 tiles of only 4 (K = 128) k-chunks,
+# and its 256 KiB of stores per tile ran after its MFMAs, not beside them.
+K_RESIDENT = True
+K_RESIDENT_MIN_N = 512
+_RR_OP_NAMES = ("sum", "max", "min", "product")
+
+
+def k_resident(M: int, K: int, N: int, src_a: Tensor, src_b: Tensor, pro_a: ChainCode | None,
+               pro_b: ChainCode | None, reduction) -> bool:
+    """Whether a matmul takes the K-resident row-wave kernel: K of 64 or 128,
+    whole 256-row blocks, at least K_RESIDENT_MIN_N columns in whole
+    128-column chunks, an output below 2 GiB, A read along rows and B along
+    K (n-major), both with
+    16-byte aligned rows, no B prologue, and an A prologue whose operands
+    are fixed per row (or none).  A row-reduction epilogue (the matmul ->
+    reduction extension) is computed in the same kernel.  The choice does
+    not depend on the batch size, so a batched program sums in the same
+    order as the same program alone."""
+    if not K_RESIDENT or pro_b is not None:
+        return False
+    if reduction is not None and reduction.op not in _RR_OP_NAMES:
+        return False
+    if K not in (64, 128) or M % 256 or N % 128 or N < K_RESIDENT_MIN_N:
+        return False
+    if M * N * 4 >= 2**31:  # the stores address the output by 32-bit byte offsets
+        return False
+    strides = (src_a.row_stride, src_a.col_stride, src_b.row_stride, src_b.col_stride)
+    if not all(isinstance(x, int) for x in strides):
+        return False
+    if src_a.col_stride != 1 or src_a.row_stride % 4 or src_b.row_stride != 1 or src_b.col_stride % 4:
+        return False
+    if not dma_offsets_fit(128, K, src_b.col_stride):
+        return False
+    return pro_a is None or pro_a.external_axes() <= {"row"}
+
+
+def k_resident_chunks(M: int, N: int, batch: int = 1) -> int:
+    """128-column chunks each workgroup of the K-resident kernel walks: as
+    many as possible while the grid still gives every compute unit a
+    workgroup -- the columns split into the fewest equal groups (a divisor
+    of the chunk count) that fill NUM_CUS with the batch's row blocks.  The
+    split does not change any sum's order."""
+    total = N // 128
+    want = ceil_div(NUM_CUS, batch * (M // 256))
+    groups = next((d for d in range(1, total + 1) if total % d == 0 and d >= want), total)
+    return total // groups
+
+
 def load_spread(*prologues: ChainCode | None) -> int:
     """Spread parts for a mainloop whose A / B prologues are ``prologues``."""
     return LOAD_SPREAD if any(gathers_full_operands(p) for p in prologues) else 0
@@ -366,6 +420,9 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
     if row_waves(M, K, N, src_a, src_b, pro_a, pro_b, decision.reduction):
         return _assemble_row_waves(decision, function_name, src_a, src_b, pro_a, value_expr, slots, out_key,
                                    extras, helpers, M, K, N)
+    if k_resident(M, K, N, src_a, src_b, pro_a, pro_b, decision.reduction):
+        return _assemble_k_resident(decision, function_name, src_a, src_b, pro_a, value_expr, slots, out_key,
+                                    extras, helpers, M, K, N, batch)
 
     full_gather = gathers_full_operands(pro_a) or gathers_full_operands(pro_b)
     tile = b_tile_for(select_tile_config(M, K, N, batch=batch, wide=WIDE_TILES and not full_gather), src_b, K, N)
@@ -509,6 +566,53 @@ def _assemble_row_waves(decision: DecisionView, function_name: str | None, src_a
         dims=(M, K, N),
         grid=(1, M // MatmulRowWavesFragment.TILE_M, 1),
         threads=(MatmulRowWavesFragment.THREADS, 1, 1),
+        ops=decision.ops,
+        strategy=decision.strategy,
+    )
+
+
+def _assemble_k_resident(decision: DecisionView, function_name: str | None, src_a: Tensor, src_b: Tensor,
+                         pro_a: ChainCode | None, value_expr: str | None, slots: dict[str, int], out_key: str,
+                         extras: Extras, helpers: list[str], M: int, K: int, N: int, batch: int) -> KernelGroup:
+    """The matmul as one MatmulKResidentFragment (``k_resident`` holds)."""
+    prologue = None
+    if pro_a is not None:
+        if gathers(pro_a):
+            prologue = ("gather", pro_a.gather_lambda(), pro_a.apply_lambda())
+        else:
+            prologue = ("transform", pro_a.lambda_transform())
+    red = decision.reduction
+    # a row reduction completes inside the workgroup: it walks whole rows
+    chunks = k_resident_chunks(M, N, batch) if red is None else N // 128
+    red_keys = (red.out.buffer_key,) if red is not None else ()
+    frag = MatmulKResidentFragment(
+        a_name=param_name(src_a.buffer_key),
+        b_name=param_name(src_b.buffer_key),
+        c_name=param_name(out_key),
+        a_row_stride=src_a.row_stride,
+        b_col_stride=src_b.col_stride,
+        K=K,
+        chunks=chunks,
+        prologue=prologue,
+        value_expr=value_expr,
+        reduction=(red.op, param_name(red.out.buffer_key)) if red is not None else None,
+    )
+    ctx = CodegenContext(
+        function_name=function_name or f"matmul_{decision.anchor.out.name}_fused",
+        buffers=(*(input_param(k) for k in slots), output_param(out_key), *extras.buffers,
+                 *(output_param(k) for k in red_keys)),
+        dims=("M", "K", "N"),
+        tg_x=MatmulKResidentFragment.THREADS,
+        tg_y=1,
+        threadgroup_decls=(lds_decl("B_tile", (2, MatmulKResidentFragment.TILE_N, K)),),
+        helpers=tuple(helpers),
+    )
+    return KernelGroup(
+        kernel=Kernel(fragments=(frag,), ctx=ctx),
+        bindings=(*slots, out_key, *extras.bindings, *red_keys),
+        dims=(M, K, N),
+        grid=(N // (MatmulKResidentFragment.TILE_N * chunks), M // MatmulKResidentFragment.TILE_M, 1),
+        threads=(MatmulKResidentFragment.THREADS, 1, 1),
         ops=decision.ops,
         strategy=decision.strategy,
     )

@@ -74,13 +74,20 @@ def check_matmul(
         over = err > stated_k * mag + rounding
         assert not over.any(), (
             f"{what}: {int(over.sum())} elements over the stated matmul bar in rows {r0}..; "
-            f"max err {err.max():.3e}"
+            f"max err {err.max():.3e}; first (row, col, got, ref): {_first_bad(over, got, ref, r0)}"
         )
         over = err > tight_k * mag + rounding
         assert not over.any(), (
             f"{what}: {int(over.sum())} elements over the float32 accumulation bound in rows {r0}..; "
             f"first at {np.argwhere(over)[0] + [r0, 0]}, max err {err.max():.3e}"
         )
+
+
+def _first_bad(over: np.ndarray, got: np.ndarray, ref: np.ndarray, r0: int, n: int = 12) -> list:
+    """The first ``n`` (row, col, got, ref) where ``over`` holds, rows
+    counted from the block at ``r0``."""
+    return [(int(r) + r0, int(c), float(got[r0 + r, c]), round(float(ref[r, c]), 6))
+            for r, c in np.argwhere(over)[:n]]
 
 
 def check_matmul_product(

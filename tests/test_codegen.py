@@ -157,9 +157,12 @@ WAIT_CASES = {
 @pytest.mark.parametrize("name", sorted(WAIT_CASES))
 def test_direct_to_lds_kernels_wait_for_every_memory_operation(name, monkeypatch):
     # A direct-to-LDS chunk shares the vector-memory counter with the
-    # epilogue's stores, and the two do not retire in issue order, so the
-    # only safe wait before the barrier that publishes a chunk is a full
-    # s_waitcnt(0): a partial count can pass with the chunk still in flight.
+    # epilogue's stores and with ordinary loads, and they do not retire in
+    # issue order, so the only safe wait before the barrier that publishes a
+    # chunk is a full s_waitcnt(0): a partial count can pass with the chunk
+    # still in flight (a vmcnt(8) that counted the K-resident kernel's A
+    # loads, issued after its first B chunk, let some waves read that chunk
+    # before it had landed: 32 wrong elements in one of C5's 32 heads).
     # Checked in every form a wait can take in the kernel's whole source
     # (the device library included): the builtin and inline asm.
     from metellus_amd.compute.matmul import config
@@ -170,8 +173,11 @@ def test_direct_to_lds_kernels_wait_for_every_memory_operation(name, monkeypatch
         monkeypatch.setattr(config, "PERSISTENT", True)
         monkeypatch.setattr(config, "PERSISTENT_CAPACITY", capacity)
         monkeypatch.setattr(config, "STREAM_K", stream_k)
-    dma = [g for g in compile_program(build()) if "mt_tile_dma<" in g.kernel.source.split('extern "C"')[-1]]
+    body = lambda g: g.kernel.source.split('extern "C"')[-1]
+    dma = [g for g in compile_program(build()) if "mt_tile_dma<" in body(g) or "mt_kr_dma<" in body(g)]
     assert dma
+    if name == "attention":  # Q @ K^T on K-resident rows, P @ V LDS-tiled
+        assert sum("mt_kr_dma<" in body(g) for g in dma) == 1 and sum("mt_tile_dma<" in body(g) for g in dma) == 1
     if loop is not None:
         assert any(marker in g.kernel.source.split('extern "C"')[-1] for g in dma), name
     for g in dma:
@@ -265,3 +271,18 @@ def test_plain_divisor_split_is_workgroup_uniform(monkeypatch):
     assert all(s.endswith(") ? 1 : 0) != 0;") and "all_plain<" in s for s in split)
     assert "if (mt_plain) {" in body
     assert hip_backend.compile_only(g.kernel.source) > 0
+
+
+def test_asm_stores_keep_their_data_registers():
+    """A 128-bit store reads its data registers after it issues.  The
+    compiler inserts the wait states for the stores it emits, but not for a
+    store inside inline asm (nor, on MI355X, for a buffer store with an
+    SGPR soffset: C5 S lost the first element of 16-32 stores a run to the
+    next row's value written right behind them).  Every store the device
+    library issues from inline asm is followed by its own s_nop."""
+    from metellus_amd.compute.fragments import device_header
+
+    src = device_header()
+    stores = re.findall(r'asm volatile\(\s*"((?:global|buffer)_store[^"]*)"', src)
+    assert len(stores) >= 3, stores
+    assert all(st.endswith("\\n\\ts_nop 1") for st in stores), stores

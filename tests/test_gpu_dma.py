@@ -20,7 +20,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _both(make, monkeypatch, outputs):
-    """(register-path env, direct-to-LDS env, direct-to-LDS groups)."""
+    """(register-path env, direct-to-LDS env, direct-to-LDS groups), on the
+    LDS-tiled kernels (the K-resident kernel loads B directly either way)."""
+    monkeypatch.setattr(mm, "K_RESIDENT", False)
     monkeypatch.setattr(mm, "DMA_LOADS", False)
     ref = run(make(), outputs=outputs).env
     monkeypatch.setattr(mm, "DMA_LOADS", True)

@@ -93,10 +93,12 @@ def test_fused_row_reduction(op, shape, monkeypatch):
         np.testing.assert_allclose(got["local"], oracle, rtol=1e-4 * np.sqrt(shape[1]), atol=1e-5)
 
 
-@pytest.mark.parametrize("form", ["workspace", "local"])
+@pytest.mark.parametrize("form", ["workspace", "local", "k-resident"])
 def test_attention_heads_batched(form, monkeypatch):
     """C5 at 512 x 64 for 6 heads in one batched launch per kernel: with the
-    row max in the score kernel every output is the reference partition's."""
+    row max in the score kernel every output is the reference partition's
+    (the LDS-tiled kernel in both of its forms, and the K-resident kernel)."""
+    monkeypatch.setattr(mm, "K_RESIDENT", form == "k-resident")
     monkeypatch.setattr(mm, "rr_local", lambda *a, **k: form == "local")
     heads = 6
     make = lambda: [gpu_cases.attention_head(512, 64, head=h, heads=heads) for h in range(heads)]

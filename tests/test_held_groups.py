@@ -16,9 +16,10 @@ from tests.gpu_cases import attention_head, mlp_block, plain_matmul
 
 @pytest.fixture(autouse=True)
 def _lds_tiled(monkeypatch):
-    """C5 P @ V on the LDS-tiled mainloop these tests are about (it takes the
-    row-owning-wave kernel by default)."""
+    """C5 P @ V and Q @ K^T on the LDS-tiled mainloop these tests are about
+    (they take the row-owning-wave and the K-resident kernels by default)."""
     monkeypatch.setattr(mm, "ROW_WAVES", False)
+    monkeypatch.setattr(mm, "K_RESIDENT", False)
 
 
 def _body(group) -> str:

@@ -132,7 +132,36 @@ def test_reference_partition_with_the_flag_off(monkeypatch):
     ]
 
 
-def test_attention_row_max_joins_the_score_kernel(monkeypatch):
+def test_attention_row_max_joins_the_k_resident_score_kernel(monkeypatch):
+    """C5's S = Q @ K^T takes the K-resident row waves; with the extension
+    its row max is computed there too: every workgroup walks whole rows
+    (grid x = 1 for any batch size), lanes fold their columns in order and
+    the 16 lanes of a row combine by an xor-butterfly -- no LDS, no
+    workspace."""
+    for batch in (32, 1):
+        gs = _groups(gpu_cases.attention_head(2048, 128, heads=32), True, monkeypatch, batch=batch)
+        assert [g.strategy for g in gs] == [
+            FusionStrategy.MATMUL_REDUCTION_EPILOGUE,
+            FusionStrategy.ELEMENTWISE_CHAIN,
+            FusionStrategy.STANDALONE_REDUCTION,
+            FusionStrategy.ELEMENTWISE_PROLOGUE_MATMUL,
+        ]
+        s = gs[0]
+        assert [op.out.name for op in s.ops] == ["S", "Ss", "m1"] and s.bindings == ("Q", "K", "Ss", "m1")
+        assert s.grid == (1, 8, 1) and s.kernel.workspace_bytes == 0
+        src = s.kernel.batched().source if batch > 1 else s.kernel.source
+        body = src.split('extern "C"')[-1]
+        assert "mt_kr_chunk<128>(" in body and "for (unsigned ch = 0; ch < 16u; ++ch)" in body
+        assert "mt_red[i] = mt_rr_op<1>(mt_red[i], mt_o[j]);" in body
+        assert [f"mt_xor_lanes<{m}u>(mt_red[i])" in body for m in (1, 2, 4, 8)] == [True] * 4
+        assert "row_red" not in body and "mt_rr_finish<" not in body
+        assert hip_backend.compile_only(src) > 0
+
+
+def test_attention_row_max_joins_the_lds_tiled_score_kernel(monkeypatch):
+    from metellus_amd.orchestrator.assembly import matmul as mm
+
+    monkeypatch.setattr(mm, "K_RESIDENT", False)
     gs = _groups(gpu_cases.attention_head(2048, 128, heads=32), True, monkeypatch, batch=32)
     assert [g.strategy for g in gs] == [
         FusionStrategy.MATMUL_REDUCTION_EPILOGUE,
@@ -154,7 +183,11 @@ def test_attention_row_max_joins_the_score_kernel(monkeypatch):
 
 def test_few_row_blocks_combine_across_workgroups(monkeypatch):
     """Two row blocks of four column tiles: every tile runs in its own
-    workgroup and the row blocks are combined through the workspace."""
+    workgroup and the row blocks are combined through the workspace (the
+    LDS-tiled kernel; K-resident rows off)."""
+    from metellus_amd.orchestrator.assembly import matmul as mm
+
+    monkeypatch.setattr(mm, "K_RESIDENT", False)
     gs = _groups(gpu_cases.attention_head(512, 64), True, monkeypatch)
     s = gs[0]
     assert s.grid == (4, 2, 1)
