@@ -51,6 +51,75 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 
 
+def source_sha16(source: str) -> str:
+    """First 16 hex digits of the SHA-256 of a kernel's source as launched:
+    ties a profile's counters to the exact kernel a bench line times."""
+    import hashlib
+
+    return hashlib.sha256(source.encode()).hexdigest()[:16]
+
+
+class GpuSensors:
+    """The GPU's hwmon readings (graphics and memory clock, power,
+    temperatures), found through its PCI bus id, sampled every ~2 ms by a
+    background thread while ``with`` is active.  Everything is optional: on
+    a machine without readable hwmon files the summary is None."""
+
+    FILES = {"sclk_mhz": ("freq1_input", 1e-6), "mclk_mhz": ("freq2_input", 1e-6),
+             "power_w": ("power1_average", 1e-6), "power_input_w": ("power1_input", 1e-6),
+             "temp_edge_c": ("temp1_input", 1e-3), "temp_junction_c": ("temp2_input", 1e-3),
+             "temp_mem_c": ("temp3_input", 1e-3)}
+
+    def __init__(self, pci_bus_id: str):
+        import glob
+
+        self.paths = {}
+        for d in glob.glob(f"/sys/bus/pci/devices/{pci_bus_id.lower()}/hwmon/hwmon*"):
+            for key, (fname, scale) in self.FILES.items():
+                f = os.path.join(d, fname)
+                if os.access(f, os.R_OK):
+                    self.paths[key] = (f, scale)
+        self.samples = {k: [] for k in self.paths}
+        self._stop = None
+
+    def _read(self):
+        for key, (f, scale) in self.paths.items():
+            try:
+                with open(f) as fh:
+                    self.samples[key].append(float(fh.read().strip()) * scale)
+            except (OSError, ValueError):
+                pass
+
+    def __enter__(self):
+        import threading
+
+        if not self.paths:
+            return self
+        self._stop = threading.Event()
+
+        def loop():
+            while not self._stop.is_set():
+                self._read()
+                self._stop.wait(0.002)
+
+        self._thread = threading.Thread(target=loop, daemon=True)
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        if self._stop is not None:
+            self._stop.set()
+            self._thread.join()
+
+    def summary(self) -> dict | None:
+        out = {}
+        for key, v in self.samples.items():
+            if v:
+                out[key] = {"min": round(min(v), 1), "mean": round(float(np.mean(v)), 1), "max": round(max(v), 1),
+                            "samples": len(v)}
+        return out or None
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -161,6 +230,9 @@ class Prepared:
         for i in range(len(self.groups)):
             self.launch(i)
 
+    def source_sha16(self, i: int) -> str:
+        return source_sha16(self.groups[i].kernel.source)
+
     def download(self, key, shape):
         return self.env[key].numpy(shape, np.float32)
 
@@ -214,6 +286,9 @@ class PreparedBatch:
             k.handle, self.tables[i], g.dims, k.dims_slot_index,
             (g.grid[0], g.grid[1], g.grid[2] * self.B), g.threads, timed=timed, workspace=k.workspace_bytes,
         )
+
+    def source_sha16(self, i: int) -> str:
+        return source_sha16(self.groups[i].kernel.batched().source)
 
     def release(self):
         for env in self.envs:
@@ -314,6 +389,7 @@ def time_kernels(prep: Prepared, steps: int, warmup: int, flusher, label: str) -
             {
                 "kernel": g.kernel.function_name,
                 "config": label,
+                "source_sha16": prep.source_sha16(i),
                 "strategy": g.strategy.value,
                 "grid": list(g.grid),
                 "threads": list(g.threads),
@@ -787,23 +863,34 @@ def fragment_benches(steps: int, flusher) -> list[dict]:
     return out
 
 
-def read_profile_traffic(config: str, kernel: str, name: str = "bench_kernels_pmc.txt") -> float | None:
+PMC_PROFILE = "bench_kernels_pmc.txt"
+
+
+def read_profile_traffic(config: str, kernel: str, sha16: str, name: str = PMC_PROFILE) -> dict:
     """HBM bytes per launch of ``kernel`` in ``config`` from the committed
-    rocprofv3 PMC summary: its table row ``config  kernel  algorithmic
-    read written ...`` (FETCH_SIZE and WRITE_SIZE, copy-kernel calibrated),
-    read + written.  None when the summary has no such row."""
+    rocprofv3 PMC summary: its table row ``config  kernel  source-sha16
+    algorithmic read written ...`` (FETCH_SIZE and WRITE_SIZE, copy-kernel
+    calibrated), read + written.  The figure is used only when the row's
+    source hash is ``sha16``, the hash of the kernel this run launches: a
+    profile of an older version of the kernel gives ``traffic`` None and
+    says so."""
     import re
 
     path = os.path.join(ROOT, "profiles", name)
+    src = {"file": f"profiles/{name}", "kernel_source_sha16": sha16, "profiled_source_sha16": None,
+           "matches": False}
     if not os.path.exists(path):
-        return None
-    pat = re.compile(r"^(.+?)\s{2,}(\S+)\s+(\(mfma\)|\d+)\s+(\d+)\s+(\d+)")
+        return {"traffic": None, "source": src}
+    pat = re.compile(r"^(.+?)\s{2,}(\S+)\s+([0-9a-f]{16})\s+(\(mfma\)|\d+)\s+(\d+)\s+(\d+)")
     with open(path, encoding="utf-8") as f:
         for line in f:
             m = pat.match(line)
-            if m and m.group(1).strip() == config and m.group(2) == kernel:
-                return float(int(m.group(4)) + int(m.group(5)))
-    return None
+            if m and m.group(1).strip() == config[:32].strip() and m.group(2) == kernel:
+                src["profiled_source_sha16"] = m.group(3)
+                src["matches"] = m.group(3) == sha16
+                traffic = float(int(m.group(5)) + int(m.group(6))) if src["matches"] else None
+                return {"traffic": traffic, "source": src}
+    return {"traffic": None, "source": src}
 
 
 C4_LABEL = "C4 MLP literal"
@@ -844,19 +931,21 @@ def headline_c4(args, flush, info) -> tuple[dict, dict]:
         warm_up(lambda timed, i=i: prep.launch(i, timed=timed), flush, args.warmup)
     hip_backend.synchronize()
     step_ms, kern_ms = [], [[] for _ in range(n)]
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        if flush is not None:
-            flush.flush()
-        hip_backend.mark(0)
-        for i in range(n):
-            prep.launch(i)
-            hip_backend.mark(i + 1)
-        step_ms.append(hip_backend.mark_elapsed(0, n))
-        for i in range(n):
-            kern_ms[i].append(hip_backend.mark_elapsed(i, i + 1))
-    hip_backend.synchronize()
-    wall = time.perf_counter() - t0
+    sensors = GpuSensors(info["pci_bus_id"])
+    with sensors:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            if flush is not None:
+                flush.flush()
+            hip_backend.mark(0)
+            for i in range(n):
+                prep.launch(i)
+                hip_backend.mark(i + 1)
+            step_ms.append(hip_backend.mark_elapsed(0, n))
+            for i in range(n):
+                kern_ms[i].append(hip_backend.mark_elapsed(i, i + 1))
+        hip_backend.synchronize()
+        wall = time.perf_counter() - t0
     hip_backend.check_workspace()
     err = check_c4(prep)
     ms = float(np.mean(step_ms))
@@ -870,14 +959,15 @@ def headline_c4(args, flush, info) -> tuple[dict, dict]:
         else:
             achieved, peak, unit = work / (mean * 1e-3) / 1e12, FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
         records.append({
-            "kernel": g.kernel.function_name, "config": C4_LABEL + " (in-step)", "strategy": g.strategy.value,
+            "kernel": g.kernel.function_name, "config": C4_LABEL + " (in-step)",
+            "source_sha16": prep.source_sha16(i), "strategy": g.strategy.value,
             "grid": list(g.grid), "threads": list(g.threads), "ms_mean": round(mean, 5),
             "ms_min": round(float(np.min(kern_ms[i])), 5), "ms_median": round(float(np.median(kern_ms[i])), 5),
             "bound": bound, "work": work, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4),
         })
     dom = max(records, key=lambda r: r["ms_mean"])
-    traffic = read_profile_traffic(C4_LABEL, dom["kernel"])
+    traffic = read_profile_traffic(C4_LABEL, dom["kernel"], dom["source_sha16"])
     line = {
         "metric": "fused-kernel fp32 TFLOP/s & HBM GB/s (% of roofline), 1×MI355X",
         "value": round(tflops, 3),
@@ -903,6 +993,10 @@ def headline_c4(args, flush, info) -> tuple[dict, dict]:
             "wall_ms_per_step_incl_flush": round(wall * 1e3 / args.steps, 4),
             "max_abs_err_vs_float64_sampled_rows": err,
             "device": info["arch"],
+            # which GPU the line ran on, and its clocks / power while the
+            # timed steps ran (hwmon, sampled every ~2 ms; None where unreadable)
+            "device_identity": {k: info[k] for k in ("pci_bus_id", "memory_clock_khz", "memory_bytes", "host")},
+            "sensors_during_steps": sensors.summary(),
             "parallelism": "1 GPU",
         },
         "roofline": {
@@ -912,7 +1006,8 @@ def headline_c4(args, flush, info) -> tuple[dict, dict]:
             "peak": dom["peak"],
             "unit": dom["unit"],
             "frac": dom["frac"],
-            "traffic": traffic,
+            "traffic": traffic["traffic"],
+            "traffic_source": traffic["source"],
         },
     }
     log(f"[bench] C4: {ms:.4f} ms/step, {tflops:.2f} TFLOP/s ({100 * tflops / FP32_MFMA_PEAK_TFLOPS:.1f}% of "
@@ -951,7 +1046,7 @@ def main() -> int:
         return 2
 
     from metellus_amd.runtime import hip_backend
-    info = hip_backend.device_info()
+    info = {**hip_backend.device_info(), **hip_backend.device_pci(), "host": os.uname().nodename}
     log(f"[bench] device {info}")
     flush = None if args.no_flush else Flusher()
 

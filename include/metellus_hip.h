@@ -40,6 +40,11 @@ int mt_device_count(int* count);
  * and peak clock in kHz. */
 int mt_device_info(char* arch, size_t arch_len, int* cu_count, int* clock_khz);
 
+/* No counterpart in the reference.  PCI bus id of device 0
+ * ("dddd:bb:dd.f"), its memory clock in kHz and its memory size in bytes
+ * (any pointer may be NULL): which GPU a measurement ran on. */
+int mt_device_pci(char* bus_id, size_t bus_id_len, int* mem_clock_khz, uint64_t* total_mem);
+
 /* create_buffer (reference: src/metal_backend.mm:94-99): nbytes must be > 0. */
 int mt_alloc(size_t nbytes, uint64_t* handle);
 

@@ -534,6 +534,18 @@ int mt_device_info(char* arch, size_t arch_len, int* cu_count, int* clock_khz) {
     return 0;
 }
 
+int mt_device_pci(char* bus_id, size_t bus_id_len, int* mem_clock_khz, uint64_t* total_mem) {
+    State& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (init_locked(s)) return 1;
+    if (bus_id && bus_id_len) MT_HIP(hipDeviceGetPCIBusId(bus_id, static_cast<int>(bus_id_len), 0));
+    hipDeviceProp_t prop;
+    MT_HIP(hipGetDeviceProperties(&prop, 0));
+    if (mem_clock_khz) *mem_clock_khz = prop.memoryClockRate;
+    if (total_mem) *total_mem = static_cast<uint64_t>(prop.totalGlobalMem);
+    return 0;
+}
+
 // Hand every cached device block back to the driver (stream-ordered).
 static int release_dev_cache(State& s) {
     for (auto& kv : s.dev_free) MT_HIP(hipFreeAsync(kv.second, s.stream));

@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "mt_init",
     "mt_device_count",
     "mt_device_info",
+    "mt_device_pci",
     "mt_alloc",
     "mt_free",
     "mt_trim",
@@ -86,6 +87,10 @@ def _load():
             "mt_device_count": ([ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
             "mt_device_info": (
                 [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)],
+                ctypes.c_int,
+            ),
+            "mt_device_pci": (
+                [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_u64)],
                 ctypes.c_int,
             ),
             "mt_alloc": ([ctypes.c_size_t, ctypes.POINTER(_u64)], ctypes.c_int),
@@ -161,6 +166,15 @@ def device_info() -> dict:
     clk = ctypes.c_int(0)
     _check(_load().mt_device_info(arch, 128, ctypes.byref(cus), ctypes.byref(clk)))
     return {"arch": arch.value.decode(), "cu_count": cus.value, "clock_khz": clk.value}
+
+
+def device_pci() -> dict:
+    """PCI bus id, memory clock (kHz) and memory size (bytes) of device 0."""
+    bus = ctypes.create_string_buffer(64)
+    mclk = ctypes.c_int(0)
+    mem = _u64(0)
+    _check(_load().mt_device_pci(bus, 64, ctypes.byref(mclk), ctypes.byref(mem)))
+    return {"pci_bus_id": bus.value.decode(), "memory_clock_khz": mclk.value, "memory_bytes": mem.value}
 
 
 def synchronize() -> None:

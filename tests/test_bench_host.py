@@ -52,3 +52,31 @@ def test_read_ceiling_grids_divide_the_sweep_sizes():
     for s in bench.SWEEP_SCALES:
         n4 = 8192 * s * 8192 * 4 // 16
         assert all(n4 % g == 0 and n4 // g >= 256 for g in bench.READ_CEILING_GRIDS)
+
+
+def test_traffic_is_read_only_for_the_profiled_kernel(tmp_path, monkeypatch):
+    """roofline.traffic comes from the committed PMC summary only when that
+    summary's row was profiled from the same kernel source (its SHA-256
+    prefix); a row from another version of the kernel gives None and names
+    both hashes."""
+    prof = tmp_path / "profiles"
+    prof.mkdir()
+    (prof / "p.txt").write_text(
+        "# header\n"
+        f"{'config':32s} {'kernel':30s} {'source':16s} {'algorithmic B':>14s} {'read B':>14s} {'written B':>12s}\n"
+        f"{'C4 MLP literal':32s} {'matmul_out_fused':30s} {'0123456789abcdef'} {'(mfma)':>14s} {4507783624:14d} {67108864:12d}\n"
+        f"{'C2 sigmoid chain 4096x4096':32s} {'elementwise_out_fused':30s} {'fedcba9876543210'} {335544320:14d} "
+        f"{268383129:14d} {67108864:12d}      0.9998\n")
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    hit = bench.read_profile_traffic("C4 MLP literal", "matmul_out_fused", "0123456789abcdef", name="p.txt")
+    assert hit["traffic"] == 4507783624 + 67108864 and hit["source"]["matches"]
+    assert hit["source"]["file"] == "profiles/p.txt"
+    stale = bench.read_profile_traffic("C4 MLP literal", "matmul_out_fused", "00000000ffffffff", name="p.txt")
+    assert stale["traffic"] is None and not stale["source"]["matches"]
+    assert stale["source"]["profiled_source_sha16"] == "0123456789abcdef"
+    hbm = bench.read_profile_traffic("C2 sigmoid chain 4096x4096", "elementwise_out_fused", "fedcba9876543210",
+                                     name="p.txt")
+    assert hbm["traffic"] == 268383129 + 67108864
+    missing = bench.read_profile_traffic("C5", "matmul_S_fused", "0123456789abcdef", name="p.txt")
+    assert missing["traffic"] is None and missing["source"]["profiled_source_sha16"] is None
+    assert bench.source_sha16("abc") == bench.source_sha16("abc") != bench.source_sha16("abd")
