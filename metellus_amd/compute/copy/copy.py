@@ -18,7 +18,14 @@ transposed views and other irregular strides.  Two forms:
   scalar 64x64 tiles, 28.7 us with 128-bit 64x64 tiles and ordinary loads
   and stores, 24.2 us with the streaming policy, 23.7 us (5.66 TB/s) with
   128x64 tiles on 256 lanes; 64x128, 128x128 (256-1024 lanes), 256x64 and
-  64x256 tiles took 24.1-34.5 us;
+  64x256 tiles took 24.1-34.5 us.  Two forms with 4 x 4 blocks transposed
+  in registers (four 128-bit loads of 4 consecutive j per lane) were slower,
+  exact both (same run, 30 launches each): stored straight from registers to
+  4 output rows, no LDS (4 lanes along i, so 64-byte reads): 25.4 us; staged
+  through LDS with 128-bit writes and reads and an XOR swizzle (512-byte
+  reads, 256-byte stores): 24.8-33.4 us over 7 tile shapes, against 24.0 for
+  this form -- a lane's 4 consecutive source rows put the rows one load
+  instruction touches 4 apart instead of adjacent;
 * ``gather`` -- any other strides: one lane per output element, the
   unravel in 32-bit arithmetic when the element count allows.
 """
