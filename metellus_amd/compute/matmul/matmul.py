@@ -90,9 +90,16 @@ class MatmulTileMappingFragment:
     """``tg`` = (column tile, row tile) of this workgroup; with ``persistent``
     it opens the tile loop (closed by ``PersistentLoopEndFragment``) and
     defines ``mt_first_tile``, ``mt_has_next``, ``mt_next_m0/n0/kb`` and the
-    item's chunk range ``mt_kb``/``mt_ke`` for the mainloop."""
+    item's chunk range ``mt_kb``/``mt_ke`` for the mainloop.
+
+    ``xcd_rows`` (one tile per workgroup only): the hardware deals workgroup
+    i (linear id x + gridDim.x y) to XCD i mod 8; the workgroups XCD c
+    receives take row tiles c xcd_rows .. (c + 1) xcd_rows - 1, all their
+    column tiles, so every A chunk is fetched into one XCD's L2 and shared
+    there (gridDim.y = 8 xcd_rows)."""
 
     persistent: PersistentTiles | None = None
+    xcd_rows: int = 0
     name: str = "tile_mapping"
     kind: str = "setup"
 
@@ -103,6 +110,14 @@ class MatmulTileMappingFragment:
 
     def render(self, ctx: CodegenContext) -> str:
         p = self.persistent
+        if p is None and self.xcd_rows:
+            return "\n".join([
+                "// XCD-grouped tile order: this XCD's workgroups share their A row tiles",
+                "const unsigned mt_lin = blockIdx.x + gridDim.x * blockIdx.y;",
+                "const unsigned mt_slot = mt_lin / 8u;",
+                f"const uint3 tg = make_uint3(mt_slot % gridDim.x, (mt_lin % 8u) * {self.xcd_rows}u + mt_slot / gridDim.x, "
+                "blockIdx.z);",
+            ])
         if p is None:
             return "const uint3 tg = make_uint3(blockIdx.x, blockIdx.y, blockIdx.z);"
         head = [

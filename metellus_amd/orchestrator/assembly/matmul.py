@@ -219,9 +219,11 @@ def dma_layouts(tile: TileConfig, srcs_a, srcs_b, pros_a, pros_b, aligned: bool)
     return dataclasses.replace(tile, a_layout="swz" if a_ok else "pad", b_layout=b_layout)
 
 
-# 16-wave tiles (config.WIDE_TILES) for matmuls whose prologues gather no
-# full-size operands and whose shape needs no bounds checks.
+# 16-wave tiles (config.WIDE_TILES) for matmuls whose shape needs no bounds
+# checks and whose prologues gather no full-size operands (or, with
+# WIDE_GATHER_TILES, also for those).
 WIDE_TILES = True
+WIDE_GATHER_TILES = False
 
 # Matmuls whose prologue gathers full-size operands issue the next k-chunk's
 # register-path loads in LOAD_SPREAD parts spread over the current chunk's
@@ -336,6 +338,20 @@ def k_resident_chunks(M: int, N: int, batch: int = 1) -> int:
     return total // groups
 
 
+# One-tile-per-workgroup matmuls whose row tiles split evenly over the 8
+# XCDs take the XCD-grouped tile order (MatmulTileMappingFragment.xcd_rows).
+XCD_TILE_ORDER = False
+
+
+def xcd_rows(grid: tuple[int, int, int]) -> int:
+    """Row tiles per XCD of the XCD-grouped order for this grid (0: the
+    plain order)."""
+    gx, gy, _ = grid
+    if not XCD_TILE_ORDER or gy % 8 or gx < 2:
+        return 0
+    return gy // 8
+
+
 def load_spread(*prologues: ChainCode | None) -> int:
     """Spread parts for a mainloop whose A / B prologues are ``prologues``."""
     return LOAD_SPREAD if any(gathers_full_operands(p) for p in prologues) else 0
@@ -425,7 +441,8 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
                                     extras, helpers, M, K, N, batch)
 
     full_gather = gathers_full_operands(pro_a) or gathers_full_operands(pro_b)
-    tile = b_tile_for(select_tile_config(M, K, N, batch=batch, wide=WIDE_TILES and not full_gather), src_b, K, N)
+    wide = WIDE_TILES and (not full_gather or WIDE_GATHER_TILES)
+    tile = b_tile_for(select_tile_config(M, K, N, batch=batch, wide=wide), src_b, K, N)
     aligned = is_aligned_shape(M, K, N, tile)
     if tile.num_threads > 512 and not aligned:
         # 16-wave tiles only without bounds checks (their masks cost registers)
@@ -490,7 +507,7 @@ def assemble_matmul(decision: DecisionView, function_name: str | None, batch: in
                                              value_expr=value_expr, check=not aligned, local=local_rr)
     fragments = (
         *((MatmulRowReduceSetupFragment(local=local_rr),) if red is not None else ()),
-        MatmulTileMappingFragment(persistent),
+        MatmulTileMappingFragment(persistent, xcd_rows=xcd_rows(grid_for(M, N, tile)) if persistent is None else 0),
         ThreadIndexFragment(tile),
         MatmulSetupFragment(config),
         mainloop,
