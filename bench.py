@@ -60,34 +60,52 @@ def source_sha16(source: str) -> str:
 
 
 class GpuSensors:
-    """The GPU's hwmon readings (graphics and memory clock, power,
-    temperatures), found through its PCI bus id, sampled every ~2 ms by a
+    """The GPU's clocks, board power and temperatures, found through its PCI
+    bus id: hwmon's inputs and the current level of ``pp_dpm_sclk`` /
+    ``pp_dpm_mclk`` (the line marked ``*``), sampled every ~1 ms by a
     background thread while ``with`` is active.  Everything is optional: on
-    a machine without readable hwmon files the summary is None."""
+    a machine without readable files the summary is None."""
 
     FILES = {"sclk_mhz": ("freq1_input", 1e-6), "mclk_mhz": ("freq2_input", 1e-6),
              "power_w": ("power1_average", 1e-6), "power_input_w": ("power1_input", 1e-6),
              "temp_edge_c": ("temp1_input", 1e-3), "temp_junction_c": ("temp2_input", 1e-3),
              "temp_mem_c": ("temp3_input", 1e-3)}
+    DPM = {"sclk_mhz": "pp_dpm_sclk", "mclk_mhz": "pp_dpm_mclk"}
+    PERIOD_S = 0.001
+    PCI_BUS_ID = ""  # the bench's GPU, set once the device is known
 
-    def __init__(self, pci_bus_id: str):
+    def __init__(self, pci_bus_id: str = ""):
         import glob
 
+        dev = f"/sys/bus/pci/devices/{(pci_bus_id or self.PCI_BUS_ID).lower()}"
         self.paths = {}
-        for d in glob.glob(f"/sys/bus/pci/devices/{pci_bus_id.lower()}/hwmon/hwmon*"):
+        for d in glob.glob(f"{dev}/hwmon/hwmon*"):
             for key, (fname, scale) in self.FILES.items():
                 f = os.path.join(d, fname)
                 if os.access(f, os.R_OK):
                     self.paths[key] = (f, scale)
+        for key, fname in self.DPM.items():
+            f = os.path.join(dev, fname)
+            if key not in self.paths and os.access(f, os.R_OK):
+                self.paths[key] = (f, None)
         self.samples = {k: [] for k in self.paths}
         self._stop = None
+
+    @staticmethod
+    def _dpm_mhz(text: str) -> float:
+        """The current level of a pp_dpm_* table (``1: 2100Mhz *``)."""
+        for line in text.splitlines():
+            if line.strip().endswith("*"):
+                return float(line.split(":", 1)[1].strip().rstrip("*").strip().lower().rstrip("mhz"))
+        raise ValueError("no current level")
 
     def _read(self):
         for key, (f, scale) in self.paths.items():
             try:
                 with open(f) as fh:
-                    self.samples[key].append(float(fh.read().strip()) * scale)
-            except (OSError, ValueError):
+                    text = fh.read()
+                self.samples[key].append(self._dpm_mhz(text) if scale is None else float(text.strip()) * scale)
+            except (OSError, ValueError, IndexError):
                 pass
 
     def __enter__(self):
@@ -100,7 +118,7 @@ class GpuSensors:
         def loop():
             while not self._stop.is_set():
                 self._read()
-                self._stop.wait(0.002)
+                self._stop.wait(self.PERIOD_S)
 
         self._thread = threading.Thread(target=loop, daemon=True)
         self._thread.start()
@@ -110,6 +128,7 @@ class GpuSensors:
         if self._stop is not None:
             self._stop.set()
             self._thread.join()
+            self._read()  # the state as the timed work ends
 
     def summary(self) -> dict | None:
         out = {}
@@ -371,10 +390,12 @@ def time_kernels(prep: Prepared, steps: int, warmup: int, flusher, label: str) -
         warm_up(lambda timed, i=i: prep.launch(i, timed=timed), flusher, warmup)
         prep.hip.synchronize()
         ms = []
-        for s in range(steps):
-            if flusher is not None:
-                flusher.flush()
-            ms.append(prep.launch(i, timed=True))
+        sensors = GpuSensors()
+        with sensors:
+            for s in range(steps):
+                if flusher is not None:
+                    flusher.flush()
+                ms.append(prep.launch(i, timed=True))
         prep.hip.check_workspace()  # raises if a stream-K launch gave up waiting
         bound, work = kernel_work(g, prep.owner)
         work *= getattr(prep, "B", 1)
@@ -402,6 +423,7 @@ def time_kernels(prep: Prepared, steps: int, warmup: int, flusher, label: str) -
                 "peak": peak,
                 "unit": unit,
                 "frac": round(achieved / peak, 4),
+                "sensors": sensors.summary(),
             }
         )
         log(f"[bench] {label} {g.kernel.function_name}: {mean:.4f} ms (median {np.median(ms):.4f})  "
@@ -931,7 +953,7 @@ def headline_c4(args, flush, info) -> tuple[dict, dict]:
         warm_up(lambda timed, i=i: prep.launch(i, timed=timed), flush, args.warmup)
     hip_backend.synchronize()
     step_ms, kern_ms = [], [[] for _ in range(n)]
-    sensors = GpuSensors(info["pci_bus_id"])
+    sensors = GpuSensors()
     with sensors:
         t0 = time.perf_counter()
         for _ in range(args.steps):
@@ -994,7 +1016,7 @@ def headline_c4(args, flush, info) -> tuple[dict, dict]:
             "max_abs_err_vs_float64_sampled_rows": err,
             "device": info["arch"],
             # which GPU the line ran on, and its clocks / power while the
-            # timed steps ran (hwmon, sampled every ~2 ms; None where unreadable)
+            # timed steps ran (sampled every ~1 ms; None where unreadable)
             "device_identity": {k: info[k] for k in ("pci_bus_id", "memory_clock_khz", "memory_bytes", "host")},
             "sensors_during_steps": sensors.summary(),
             "parallelism": "1 GPU",
@@ -1047,6 +1069,7 @@ def main() -> int:
 
     from metellus_amd.runtime import hip_backend
     info = {**hip_backend.device_info(), **hip_backend.device_pci(), "host": os.uname().nodename}
+    GpuSensors.PCI_BUS_ID = info["pci_bus_id"]
     log(f"[bench] device {info}")
     flush = None if args.no_flush else Flusher()
 

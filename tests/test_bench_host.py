@@ -80,3 +80,16 @@ def test_traffic_is_read_only_for_the_profiled_kernel(tmp_path, monkeypatch):
     missing = bench.read_profile_traffic("C5", "matmul_S_fused", "0123456789abcdef", name="p.txt")
     assert missing["traffic"] is None and missing["source"]["profiled_source_sha16"] is None
     assert bench.source_sha16("abc") == bench.source_sha16("abc") != bench.source_sha16("abd")
+
+
+def test_sensor_parsing_and_absence(tmp_path):
+    """The current clock level of a pp_dpm_* table is the line marked '*';
+    a machine without the GPU's sysfs files gives no sensor summary."""
+    assert bench.GpuSensors._dpm_mhz("0: 500Mhz\n1: 2105Mhz *\n2: 2400Mhz\n") == 2105.0
+    assert bench.GpuSensors._dpm_mhz("0: 2000Mhz *\n") == 2000.0
+    with pytest.raises(ValueError):
+        bench.GpuSensors._dpm_mhz("0: 500Mhz\n1: 2400Mhz\n")
+    s = bench.GpuSensors("0000:ff:1f.7")
+    with s:
+        pass
+    assert s.paths == {} and s.summary() is None

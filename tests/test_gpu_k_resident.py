@@ -232,3 +232,46 @@ def test_random_k_resident_programs(seed):
     ref = {"none": y, "relu": np.maximum(y, 0.0), "scale": -0.5 * y}[epi]
     bound = (1e-4 * np.sqrt(K) + 4e-7) * (np.abs(a64) @ np.abs(b64)) * (0.5 if epi == "scale" else 1.0) + 1e-30
     assert np.all(np.abs(got - ref) <= bound), float(np.max(np.abs(got - ref) / bound))
+
+
+@pytest.mark.parametrize("axis", ["col", "row"])
+def test_epilogue_with_a_broadcast_operand(axis, monkeypatch):
+    """Y = A @ B^T + bias with the bias per output column (a row vector) or
+    per output row (a column vector): the K-resident epilogue reads it by the
+    (row, col) each stored element has -- against the float64 product plus
+    the bias, at the matmul bar, and against the LDS-tiled kernel."""
+    M, K, N = 512, 128, 1024
+    rng = np.random.default_rng(73)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    bs = rng.standard_normal((N, K)).astype(np.float32)
+    bias = rng.standard_normal(N if axis == "col" else M).astype(np.float32)
+
+    def program():
+        ops = Operations()
+        ops.from_numpy(a, "A")
+        ops.from_numpy(bs, "Bs")
+        ops.transpose("Bs", out="B")
+        ops.from_numpy(bias, "bias")
+        if axis == "col":
+            ops.reshape("bias", (1, N), out="bv")
+            bc = "row"  # one value per column, broadcast over the rows
+        else:
+            ops.reshape("bias", (M, 1), out="bv")
+            bc = "col"
+        ops.matmul(a="A", b="B", out="Y0")
+        ops.elementwise("add", out="Y", operands=("Y0", "bv"), y_broadcast=bc)
+        return ops
+
+    got = {}
+    for on in (True, False):
+        monkeypatch.setattr(mm, "K_RESIDENT", on)
+        print(f"k-resident: bias per {axis}, on={on}", flush=True)
+        res = run(program(), outputs=("Y",))
+        assert len(res.groups) == 1 and ("mt_kr_chunk<" in _body(res)) == on
+        got[on] = res.env["Y"]
+    y64 = a.astype(np.float64) @ bs.T.astype(np.float64)
+    y64 = y64 + (bias[None, :] if axis == "col" else bias[:, None])
+    mag = np.abs(a).astype(np.float64) @ np.abs(bs.T).astype(np.float64) + np.abs(y64)
+    bound = (1e-4 * np.sqrt(K)) * mag + 1e-30
+    assert np.all(np.abs(got[True] - y64) <= bound)
+    np.testing.assert_allclose(got[True], got[False], rtol=1e-4, atol=1e-4)
