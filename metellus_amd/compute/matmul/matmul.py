@@ -868,7 +868,7 @@ class MatmulKResidentFragment:
             "// row i of a finished column half h (blocks 4h .. 4h + 3) of the chunk",
             "// at columns col_base: the epilogue, then one 128-bit buffer store at",
             "// this lane's byte offset plus a wave-uniform one",
-            f"const mt_u32x4 mt_rs = mt_raw_buffer({c});",
+            f"const mt_u32x4 mt_rs = mt_raw_buffer({c}, M * N * 4u);",
             "const unsigned mt_voff = ((tile_m0 + wave * 16u + 4u * (lane >> 4)) * N + mt_n0 + 4u * (lane & 15u)) * 4u;",
             "const auto mt_store_row = [&](int h, int i, unsigned col_base) {",
             "    const unsigned row = tile_m0 + wave * 16u + 4u * (lane >> 4) + (unsigned)i;",

@@ -1142,14 +1142,15 @@ MT_INLINE void mt_kr_chunk(const mt_f32x4 (&a)[K / 16], const float* __restrict_
     __builtin_amdgcn_s_setprio(0);
 }
 
-// Raw buffer access to an output: one descriptor per workgroup (32-bit data,
-// stride 0, the whole 4 GiB range), so a store takes one per-lane byte
-// offset and one wave-uniform one instead of a 64-bit address per lane.
+// Raw buffer access to an output of `bytes` bytes: one descriptor per
+// workgroup (32-bit data, stride 0), so a store takes one per-lane byte
+// offset and one wave-uniform one instead of a 64-bit address per lane; the
+// hardware drops a store beyond the range instead of writing it.
 typedef unsigned mt_u32x4 __attribute__((ext_vector_type(4)));
 
-MT_INLINE mt_u32x4 mt_raw_buffer(const void* p) {
+MT_INLINE mt_u32x4 mt_raw_buffer(const void* p, unsigned bytes) {
     const unsigned long long a = mt_uniform_addr(static_cast<const float*>(p));
-    return mt_u32x4{(unsigned)a, (unsigned)(a >> 32) & 0xffffu, 0xffffffffu, 0x00020000u};
+    return mt_u32x4{(unsigned)a, (unsigned)(a >> 32) & 0xffffu, (unsigned)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000u};
 }
 
 // 16 bytes to rs + voff + soff (POLICY 16: sc1, device scope, written
