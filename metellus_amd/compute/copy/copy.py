@@ -17,8 +17,8 @@ transposed views and other irregular strides.  Two forms:
   lane per output element gathering through the strides, 35.1 us with
   scalar 64x64 tiles, 28.7 us with 128-bit 64x64 tiles and ordinary loads
   and stores, 24.2 us with the streaming policy, 23.7 us (5.66 TB/s) with
-  128x64 tiles on 256 lanes; 64x128, 128x128 (256-1024 lanes), 256x64 and
-  64x256 tiles took 24.1-34.5 us.  Two forms with 4 x 4 blocks transposed
+  128x64 tiles on 256 lanes, 23.6 us (5.69 TB/s) on 512 lanes (24.1 on 1024);
+  64x128, 128x128 (256-1024 lanes), 256x64 and 64x256 tiles took 24.1-34.5 us.  Two forms with 4 x 4 blocks transposed
   in registers (four 128-bit loads of 4 consecutive j per lane) were slower,
   exact both (same run, 30 launches each): stored straight from registers to
   4 output rows, no LDS (4 lanes along i, so 64-byte reads): 25.4 us; staged
@@ -41,7 +41,7 @@ from metellus_amd.compute.fragments import CodegenContext, TgmemAccess
 # axis (j, the output's contiguous one), TRANSPOSE_LANES lanes per workgroup.
 TRANSPOSE_TILE_I = 128
 TRANSPOSE_TILE_J = 64
-TRANSPOSE_LANES = 256
+TRANSPOSE_LANES = 512
 TRANSPOSE_PAD = 1  # LDS row padding: column reads hit distinct banks
 # Streaming cache policy of the 128-bit form: nontemporal loads and
 # device-scope stores (written through L2), as the flat elementwise streams.
