@@ -64,7 +64,12 @@ class GpuSensors:
     bus id: hwmon's inputs and the current level of ``pp_dpm_sclk`` /
     ``pp_dpm_mclk`` (the line marked ``*``), sampled every ~1 ms by a
     background thread while ``with`` is active.  Everything is optional: on
-    a machine without readable files the summary is None."""
+    a machine without readable files the summary is None.  A sample covers
+    whatever the GPU did in that millisecond: around the per-kernel timing
+    loops that includes each launch's cache flush and host synchronisation,
+    so short kernels' clock readings are averages with idle gaps, lower than
+    the clock the kernel itself ran at (its MFMA rate bounds that from
+    below); the C4 steps run back to back and are read cleanly."""
 
     FILES = {"sclk_mhz": ("freq1_input", 1e-6), "mclk_mhz": ("freq2_input", 1e-6),
              "power_w": ("power1_average", 1e-6), "power_input_w": ("power1_input", 1e-6),
@@ -1019,6 +1024,8 @@ def headline_c4(args, flush, info) -> tuple[dict, dict]:
             # timed steps ran (sampled every ~1 ms; None where unreadable)
             "device_identity": {k: info[k] for k in ("pci_bus_id", "memory_clock_khz", "memory_bytes", "host")},
             "sensors_during_steps": sensors.summary(),
+            "sensors_scope": "every ~1 ms over the timed steps (back to back); per_kernel sensors span each "
+                             "kernel's timing loop, flushes and host waits included",
             "parallelism": "1 GPU",
         },
         "roofline": {
